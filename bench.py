@@ -1,0 +1,241 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X fp8 block-scale MoE operator (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode_t16]
+
+A step is one call of the operator (routing -> permutation -> GEMM1+SwiGLU ->
+GEMM2 -> combine) on one batch of synthetic tokens, all inputs resident in HBM.
+Each timed step starts cold: a 512 MiB buffer is rewritten before it (outside
+the timed interval), which evicts the 256 MB Infinity Cache.  Per-step device
+time comes from HIP events recorded around the C-ABI call; the library also
+records one event between consecutive kernels (the ``stage_events`` argument),
+which gives every kernel's device time live, on the stream it runs on.
+
+Prints ONE JSON line.  Headline: T=16 decode (H=7168, I=2048, 32 local experts),
+in us/call; the T=8192 large-prefill line and the other synthetic workloads
+are reported inside the same object.  ``cpu_baseline`` times the CPU oracle
+(fp32 torch, all local experts dequantised up front like the contest reference)
+on the host cores for one call of the headline workload.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "rocm-flashinfer-contest_amd"))
+
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+FP8_PEAK = 5.0e15          # dense fp8 MFMA FLOP/s, MI355X
+FLUSH_BYTES = 512 << 20
+
+
+class StageEvents:
+    """HIP events owned by torch (same HIP runtime as the library); their raw
+    hipEvent_t handles are passed to the library, which records them between kernels."""
+
+    def __init__(self, n):
+        import torch
+        self.events = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        for e in self.events:
+            e.record()                      # materialise the underlying hipEvent_t
+        torch.cuda.synchronize()
+        self.arr = (ctypes.c_void_p * n)(*[e.cuda_event for e in self.events])
+
+    def ptr(self, first):
+        return ctypes.addressof(self.arr) + first * ctypes.sizeof(ctypes.c_void_p)
+
+    def ms(self, a, b):
+        return float(self.events[a].elapsed_time(self.events[b]))
+
+
+def work_counts(expert_offsets, T, H, I):
+    """Algorithmic HBM bytes and fp8 flops of one call from the routing counts."""
+    counts = [int(expert_offsets[i + 1] - expert_offsets[i]) for i in range(len(expert_offsets) - 1)]
+    A = sum(1 for c in counts if c > 0)
+    P = sum(counts)
+    w13 = 2 * I * H + (2 * I // 128) * (H // 128) * 4
+    w2 = H * I + (H // 128) * (I // 128) * 4
+    per_token = H + (H // 128) * 4 + 256 * 4 + H * 2
+    return dict(active_experts=A, pairs=P, bytes=A * (w13 + w2) + T * per_token + 512,
+                flops=P * (2 * H * 2 * I + 2 * I * H),
+                gemm1_bytes=A * w13 + P * (H + (H // 128) * 4) + P * I * 4,
+                gemm1_flops=P * 2 * H * 2 * I,
+                gemm2_bytes=A * w2 + P * I * 4 + P * H * 4,
+                gemm2_flops=P * 2 * I * H)
+
+
+def measure(wl, weights, steps, warmup, flush):
+    import torch
+    from moe_fp8 import workloads as W
+    from moe_fp8._abi import NUM_STAGE_EVENTS, STAGES
+    from moe_fp8.main import Runner
+
+    act = W.make_activations(wl, device="cuda")
+    dbg = {}
+    runner = Runner(*act, *weights, 0, W.RSF, debug=dbg)
+    runner()
+    torch.cuda.synchronize()
+    eo = dbg["expert_offsets"].cpu().tolist()
+    runner.args.topk_ids = runner.args.topk_weights = runner.args.expert_offsets = runner.args.permuted_tokens = None
+    for _ in range(warmup):
+        flush.zero_()
+        runner()
+    torch.cuda.synchronize()
+    ev = StageEvents(steps * NUM_STAGE_EVENTS)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        flush.zero_()
+        runner(stage_events=ev.ptr(i * NUM_STAGE_EVENTS))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_step, stages = [], {s: [] for s in STAGES}
+    for i in range(steps):
+        b = i * NUM_STAGE_EVENTS
+        per_step.append(ev.ms(b, b + NUM_STAGE_EVENTS - 1) * 1e3)
+        for j, s in enumerate(STAGES):
+            stages[s].append(ev.ms(b + j, b + j + 1) * 1e3)
+    # warm back-to-back (no flush), for reference
+    torch.cuda.synchronize()
+    e_a, e_b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e_a.record()
+    for _ in range(steps):
+        runner()
+    e_b.record()
+    torch.cuda.synchronize()
+    warm_us = e_a.elapsed_time(e_b) * 1e3 / steps
+    T = wl.T
+    H, I = W.H_FULL, W.I_FULL
+    wk = work_counts(eo, T, H, I)
+    us = statistics.median(per_step)
+    st = {s: statistics.median(v) for s, v in stages.items()}
+    res = dict(workload=wl.name, T=T, us_per_call=us, us_min=min(per_step), us_max=max(per_step),
+               us_mean=statistics.fmean(per_step), warm_us_per_call=warm_us, host_wall_s=wall,
+               stages_us=st, **wk)
+    res["tflops"] = wk["flops"] / (us * 1e-6) / 1e12
+    res["gbps"] = wk["bytes"] / (us * 1e-6) / 1e9
+    res["hbm_frac"] = wk["bytes"] / (us * 1e-6) / HBM_PEAK
+    res["mfma_frac"] = wk["flops"] / (us * 1e-6) / FP8_PEAK
+    t_roof = max(wk["bytes"] / HBM_PEAK, wk["flops"] / FP8_PEAK)
+    res["roofline_frac"] = t_roof / (us * 1e-6)
+    # dominant kernel and its own roofline
+    dom = max(("gemm1", "gemm2"), key=lambda s: st[s])
+    k_us = st[dom]
+    k_bytes, k_flops = wk[f"{dom}_bytes"], wk[f"{dom}_flops"]
+    hbm_bound = k_bytes / HBM_PEAK >= k_flops / FP8_PEAK
+    if hbm_bound:
+        ach = k_bytes / (k_us * 1e-6) / 1e9
+        roof = dict(bound="hbm", achieved=ach, peak=HBM_PEAK / 1e9, unit="GB/s", frac=ach / (HBM_PEAK / 1e9))
+    else:
+        ach = k_flops / (k_us * 1e-6) / 1e12
+        roof = dict(bound="mfma", achieved=ach, peak=FP8_PEAK / 1e12, unit="TFLOP/s", frac=ach / (FP8_PEAK / 1e12))
+    roof.update(kernel=dom, kernel_us=k_us, algorithmic_bytes=k_bytes, algorithmic_flops=k_flops, traffic=None)
+    res["roofline"] = roof
+    del runner
+    return res
+
+
+def cpu_baseline(wl, weights_cpu, threads):
+    import torch
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import moe_oracle
+    from moe_fp8 import workloads as W
+
+    torch.set_num_threads(threads)
+    act = W.make_activations(wl, device="cpu")
+    t0 = time.perf_counter()
+    moe_oracle.moe_forward(*act, *weights_cpu, 0, W.RSF, dequant_all_upfront=True)
+    dt = time.perf_counter() - t0
+    return dict(value=dt * 1e6, unit="us/call", cores=threads, kind="port",
+                sample=f"1 call of {wl.name} (T={wl.T}, H=7168, I=2048, 32 local experts): fp32 torch-CPU oracle, "
+                       f"all 32 experts dequantised up front as in the contest reference; {threads} threads")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="decode_t16")
+    ap.add_argument("--secondary", default="large_t8192")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the operator runs all 32 local experts of one expert-parallel rank on a "
+              f"single MI355X; --gpus {args.gpus} is not supported", file=sys.stderr)
+        return 2
+
+    import torch
+    from moe_fp8 import workloads as W
+
+    torch.cuda.set_device(0)
+    wls = W.workloads()
+    weights = W.make_weights(device="cuda")
+    flush = torch.empty(FLUSH_BYTES, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    head = measure(wls[args.workload], weights, args.steps, args.warmup, flush)
+    print(f"# {args.workload}: {head['us_per_call']:.1f} us/call", file=sys.stderr, flush=True)
+    sweep = {}
+    if not args.no_sweep:
+        for name, wl in wls.items():
+            if name == args.workload:
+                continue
+            r = measure(wl, weights, args.steps, args.warmup, flush)
+            print(f"# {name}: {r['us_per_call']:.1f} us/call", file=sys.stderr, flush=True)
+            sweep[name] = r
+    sec = sweep.get(args.secondary)
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+        weights_cpu = tuple(x.cpu() for x in weights)
+        cpu = cpu_baseline(wls[args.workload], weights_cpu, threads)
+        print(f"# cpu baseline: {cpu['value']:.0f} us/call on {threads} threads", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": f"moe_fp8 block-scale MoE latency, {args.workload} (T={head['T']}, H=7168, I=2048, 32 local experts)",
+        "value": round(head["us_per_call"], 3),
+        "unit": "us/call",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_mean"] / 1e3, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "T": head["T"], "H": 7168, "I": 2048, "E_local": 32,
+                   "top_k": 8, "n_group": 8, "topk_group": 4, "local_expert_offset": 0, "routed_scaling": 2.5,
+                   "active_experts": head["active_experts"], "pairs": head["pairs"], "cold_cache": True},
+        "tflops": round(head["tflops"], 3),
+        "gbps": round(head["gbps"], 1),
+        "hbm_frac": round(head["hbm_frac"], 4),
+        "mfma_frac": round(head["mfma_frac"], 5),
+        "roofline_frac": round(head["roofline_frac"], 4),
+        "stages_us": {k: round(v, 2) for k, v in head["stages_us"].items()},
+        "warm_us_per_call": round(head["warm_us_per_call"], 2),
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+    }
+    if sec is not None:
+        line["t8192"] = {k: sec[k] for k in ("us_per_call", "tflops", "gbps", "hbm_frac", "mfma_frac", "roofline_frac",
+                                           "active_experts", "pairs", "stages_us", "roofline")}
+    if sweep:
+        line["sweep"] = {k: {"us_per_call": round(v["us_per_call"], 2), "tflops": round(v["tflops"], 2),
+                             "gbps": round(v["gbps"], 1), "roofline_frac": round(v["roofline_frac"], 4),
+                             "P": v["pairs"], "A": v["active_experts"],
+                             "stages_us": {s: round(x, 1) for s, x in v["stages_us"].items()}}
+                         for k, v in sweep.items()}
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

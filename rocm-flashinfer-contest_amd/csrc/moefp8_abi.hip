@@ -1,0 +1,261 @@
+// extern "C" boundary of the gfx950 MoE operator (declared in include/moefp8.h).
+//
+// moefp8_run replaces the Python entry point solutions/moe_fp8/main.py:173-243.
+// It checks every argument on the host, carves the caller's workspace, and
+// enqueues on the caller's stream:
+//   route -> permute -> GEMM1(+SwiGLU) -> GEMM2 -> combine
+// with no host synchronisation and no allocation.  The small-T variant streams
+// weights; the large-T variant stages activations through LDS.  Both are
+// chosen by T alone, so the launch sequence is fixed for given sizes.
+#include <atomic>
+#include <cstring>
+
+#include "../../include/moefp8.h"
+#include "moefp8_device.h"
+#include "moefp8_launch.h"
+
+namespace moefp8 {
+
+// Largest T served by the weight-streaming kernels.
+constexpr int64_t kDecodeMaxT = 64;
+
+int tile_m_for(int64_t T) {
+  if (T <= kDecodeMaxT) return 16;
+  return 64;
+}
+
+struct Layout {
+  size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
+  size_t cbuf, c_q, c_plane, c_scale, c_kmax, obuf, total;
+  int64_t pmax, max_mtiles;
+};
+
+static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static Layout make_layout(int64_t T, int E_local, int H, int I) {
+  Layout L;
+  const int64_t pmax = T * (E_local < kTopK ? E_local : kTopK);
+  L.pmax = pmax;
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o = align_up(o + bytes);
+    return at;
+  };
+  L.topk_ids = take((size_t)T * kTopK * 4);
+  L.topk_w = take((size_t)T * kTopK * 4);
+  L.expert_offsets = take((size_t)(E_local + 1) * 4);
+  L.active = take((size_t)E_local * 4);
+  L.mtile_offsets = take((size_t)(E_local + 1) * 4);
+  L.info = take(64);
+  L.perm_token = take((size_t)pmax * 4);
+  L.perm_w = take((size_t)pmax * 4);
+  L.tok_slot = take((size_t)T * kTopK * 4);
+  // C between the GEMMs: fp32 [pmax, I] (small T) or, for large T, kMaxTerms e4m3 planes
+  // [pmax, I] + fp32 scales [pmax, I/128] + per-sub-tile term counts
+  const int tm = tile_m_for(T);
+  L.max_mtiles = (pmax + tm - 1) / tm + E_local;
+  L.c_plane = align_up((size_t)pmax * I);
+  const size_t c_f32 = (size_t)pmax * I * 4;
+  const size_t c_scale_bytes = align_up((size_t)pmax * (I / kBlock) * 4);
+  const size_t c_kmax_bytes = (size_t)L.max_mtiles * (tm / 16) * (I / kBlock);
+  const size_t c_split = L.c_plane * kMaxTerms + c_scale_bytes + c_kmax_bytes;
+  L.cbuf = take(c_f32 > c_split ? c_f32 : c_split);
+  L.c_q = L.cbuf;
+  L.c_scale = L.c_q + L.c_plane * kMaxTerms;
+  L.c_kmax = L.c_scale + c_scale_bytes;
+  L.obuf = take((size_t)pmax * H * 4);
+  L.total = o;
+  return L;
+}
+
+static std::atomic<int> g_cu_count[64];
+static std::atomic<int> g_arch_ok[64];  // 0 unknown, 1 gfx950, -1 other
+
+static int query_device(int* dev_out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return MOEFP8_ERR_DEVICE;
+  *dev_out = dev;
+  if (dev < 0 || dev >= 64) return MOEFP8_ERR_DEVICE;
+  if (g_arch_ok[dev].load(std::memory_order_acquire) == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return MOEFP8_ERR_DEVICE;
+    g_cu_count[dev].store(prop.multiProcessorCount, std::memory_order_relaxed);
+    const bool ok = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    g_arch_ok[dev].store(ok ? 1 : -1, std::memory_order_release);
+  }
+  return g_arch_ok[dev].load(std::memory_order_acquire) == 1 ? MOEFP8_OK : MOEFP8_ERR_DEVICE;
+}
+
+int num_compute_units() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  const int n = g_cu_count[dev].load(std::memory_order_relaxed);
+  return n > 0 ? n : 256;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// fp32 logits are read as float4 rows; 16-bit inputs element by element.
+static bool aligned_for_dtype(const void* p, int dt) {
+  return ((uintptr_t)p & (dt == 0 ? 15u : 1u)) == 0;
+}
+
+static int check_sizes(int64_t T, int E_local, int H, int I) {
+  if (T < 0 || T > (int64_t)1 << 24) return MOEFP8_ERR_SHAPE;
+  if (E_local < 1 || E_local > kEGlobal) return MOEFP8_ERR_SHAPE;
+  if (H <= 0 || I <= 0 || H % kBlock != 0 || I % kBlock != 0) return MOEFP8_ERR_SHAPE;
+  return MOEFP8_OK;
+}
+
+static int check_dtype(int dt) { return (dt >= 0 && dt <= 2) ? MOEFP8_OK : MOEFP8_ERR_DTYPE; }
+
+}  // namespace moefp8
+
+using namespace moefp8;
+
+extern "C" {
+
+int moefp8_abi_version(void) { return MOEFP8_ABI_VERSION; }
+
+const char* moefp8_strerror(int status) {
+  switch (status) {
+    case MOEFP8_OK: return "ok";
+    case MOEFP8_ERR_NULL_POINTER: return "a required pointer is NULL";
+    case MOEFP8_ERR_SHAPE: return "bad shape: need T >= 0, 1 <= E_local <= 256, H and I positive multiples of 128";
+    case MOEFP8_ERR_DTYPE: return "unsupported dtype code for routing logits or bias";
+    case MOEFP8_ERR_ALIGNMENT: return "a tensor pointer is not 16-byte aligned";
+    case MOEFP8_ERR_WORKSPACE: return "workspace is NULL or smaller than moefp8_workspace_size()";
+    case MOEFP8_ERR_LAUNCH: return "kernel launch failed";
+    case MOEFP8_ERR_DEVICE: return "current HIP device is not gfx950 or the HIP runtime failed";
+    default: return "unknown status";
+  }
+}
+
+int moefp8_workspace_size(int64_t num_tokens, int32_t num_local_experts, int32_t hidden_size,
+                          int32_t intermediate_size, size_t* bytes) {
+  if (!bytes) return MOEFP8_ERR_NULL_POINTER;
+  const int rc = check_sizes(num_tokens, num_local_experts, hidden_size, intermediate_size);
+  if (rc) return rc;
+  *bytes = make_layout(num_tokens, num_local_experts, hidden_size, intermediate_size).total;
+  return MOEFP8_OK;
+}
+
+int moefp8_route(const void* routing_logits, int32_t logits_dtype, const void* routing_bias, int32_t bias_dtype,
+                 int64_t num_tokens, float routed_scaling_factor, int32_t* topk_ids, float* topk_weights,
+                 void* stream) {
+  if (num_tokens < 0 || num_tokens > (int64_t)1 << 24) return MOEFP8_ERR_SHAPE;
+  if (check_dtype(logits_dtype) || check_dtype(bias_dtype)) return MOEFP8_ERR_DTYPE;
+  if (num_tokens == 0) return MOEFP8_OK;
+  if (!routing_logits || !routing_bias || !topk_ids || !topk_weights) return MOEFP8_ERR_NULL_POINTER;
+  if (!aligned_for_dtype(routing_logits, logits_dtype) || !aligned_for_dtype(routing_bias, bias_dtype) ||
+      ((uintptr_t)topk_ids & 3u) || ((uintptr_t)topk_weights & 3u))
+    return MOEFP8_ERR_ALIGNMENT;
+  int dev;
+  if (query_device(&dev)) return MOEFP8_ERR_DEVICE;
+  hipStream_t s = (hipStream_t)stream;
+  launch_route(routing_logits, logits_dtype, routing_bias, bias_dtype, num_tokens, routed_scaling_factor, topk_ids,
+               topk_weights, s);
+  return hipGetLastError() == hipSuccess ? MOEFP8_OK : MOEFP8_ERR_LAUNCH;
+}
+
+int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!a) return MOEFP8_ERR_NULL_POINTER;
+  const int64_t T = a->num_tokens;
+  const int E_local = a->num_local_experts, H = a->hidden_size, I = a->intermediate_size;
+  int rc = check_sizes(T, E_local, H, I);
+  if (rc) return rc;
+  if (check_dtype(a->logits_dtype) || check_dtype(a->bias_dtype)) return MOEFP8_ERR_DTYPE;
+  if (T == 0) return MOEFP8_OK;
+  if (!a->routing_logits || !a->routing_bias || !a->hidden_states || !a->hidden_states_scale ||
+      !a->gemm1_weights || !a->gemm1_weights_scale || !a->gemm2_weights || !a->gemm2_weights_scale || !a->output)
+    return MOEFP8_ERR_NULL_POINTER;
+  const void* ptrs16[] = {a->hidden_states, a->gemm1_weights, a->gemm2_weights, a->output};
+  for (const void* p : ptrs16)
+    if (!aligned16(p)) return MOEFP8_ERR_ALIGNMENT;
+  const void* ptrs4[] = {a->hidden_states_scale, a->gemm1_weights_scale, a->gemm2_weights_scale};
+  for (const void* p : ptrs4)
+    if (((uintptr_t)p & 3u) != 0) return MOEFP8_ERR_ALIGNMENT;
+  if (!aligned_for_dtype(a->routing_logits, a->logits_dtype) || !aligned_for_dtype(a->routing_bias, a->bias_dtype))
+    return MOEFP8_ERR_ALIGNMENT;
+  const Layout L = make_layout(T, E_local, H, I);
+  if (!workspace || workspace_bytes < L.total || !aligned16(workspace)) return MOEFP8_ERR_WORKSPACE;
+  int dev;
+  if (query_device(&dev)) return MOEFP8_ERR_DEVICE;
+
+  hipStream_t s = (hipStream_t)stream;
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  int* topk_ids = reinterpret_cast<int*>(ws + L.topk_ids);
+  float* topk_w = reinterpret_cast<float*>(ws + L.topk_w);
+  Plan pl;
+  pl.expert_offsets = reinterpret_cast<int*>(ws + L.expert_offsets);
+  pl.perm_token = reinterpret_cast<int*>(ws + L.perm_token);
+  pl.perm_w = reinterpret_cast<float*>(ws + L.perm_w);
+  pl.tok_slot = reinterpret_cast<int*>(ws + L.tok_slot);
+  pl.active = reinterpret_cast<int*>(ws + L.active);
+  pl.mtile_offsets = reinterpret_cast<int*>(ws + L.mtile_offsets);
+  pl.info = reinterpret_cast<int*>(ws + L.info);
+
+  Problem pb;
+  pb.hidden = a->hidden_states;
+  pb.hscale = a->hidden_states_scale;
+  pb.w13 = a->gemm1_weights;
+  pb.s13 = a->gemm1_weights_scale;
+  pb.w2 = a->gemm2_weights;
+  pb.s2 = a->gemm2_weights_scale;
+  pb.T = (int)T;
+  pb.E_local = E_local;
+  pb.H = H;
+  pb.I = I;
+
+  const int tile_m = tile_m_for(T);
+  hipEvent_t* ev = reinterpret_cast<hipEvent_t*>(a->stage_events);
+  auto mark = [&](int i) {
+    if (ev) (void)hipEventRecord(ev[i], s);
+  };
+  mark(0);
+  launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,
+               topk_ids, topk_w, s);
+  mark(1);
+  launch_permute(topk_ids, topk_w, (int)T, E_local, a->local_expert_offset, tile_m,
+                 const_cast<int*>(pl.expert_offsets), const_cast<int*>(pl.perm_token), const_cast<float*>(pl.perm_w),
+                 const_cast<int*>(pl.tok_slot), const_cast<int*>(pl.active), const_cast<int*>(pl.mtile_offsets),
+                 const_cast<int*>(pl.info), s);
+  mark(2);
+  float* obuf = reinterpret_cast<float*>(ws + L.obuf);
+  if (T <= kDecodeMaxT) {
+    const int n_slots = (int)(L.pmax < E_local ? L.pmax : E_local);
+    float* cbuf = reinterpret_cast<float*>(ws + L.cbuf);
+    launch_gemm1_decode(pb, pl, cbuf, n_slots, s);
+    mark(3);
+    launch_gemm2_decode(pb, pl, cbuf, obuf, n_slots, s);
+  } else {
+    CSplit cs;
+    cs.q = ws + L.c_q;
+    cs.plane = L.c_plane;
+    cs.scale = reinterpret_cast<float*>(ws + L.c_scale);
+    cs.kmax = ws + L.c_kmax;
+    launch_gemm1_prefill(pb, pl, tile_m, cs, (int)L.max_mtiles, s);
+    mark(3);
+    launch_gemm2_prefill(pb, pl, tile_m, cs, obuf, (int)L.max_mtiles, s);
+  }
+  mark(4);
+  launch_combine(pl, obuf, a->output, (int)T, H, s);
+  mark(5);
+
+  if (hipGetLastError() != hipSuccess) return MOEFP8_ERR_LAUNCH;
+  struct Copy {
+    void* dst;
+    const void* src;
+    size_t bytes;
+  } copies[] = {{a->topk_ids, topk_ids, (size_t)T * kTopK * 4},
+                {a->topk_weights, topk_w, (size_t)T * kTopK * 4},
+                {a->expert_offsets, pl.expert_offsets, (size_t)(E_local + 1) * 4},
+                {a->permuted_tokens, pl.perm_token, (size_t)L.pmax * 4}};
+  for (const Copy& c : copies)
+    if (c.dst && hipMemcpyAsync(c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return MOEFP8_ERR_LAUNCH;
+  return MOEFP8_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,113 @@
+// Device-side helpers shared by the gfx950 MoE kernels: operand vector types,
+// the fp8 MFMA, wavefront shuffles, OCP e4m3 encode/decode and bf16 rounding.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moefp8 {
+
+constexpr int kEGlobal = 256;
+constexpr int kTopK = 8;
+constexpr int kNGroup = 8;
+constexpr int kTopKGroup = 4;
+constexpr int kGroupSize = kEGlobal / kNGroup;
+constexpr int kBlock = 128;
+constexpr int kWave = 64;
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// D = A(16x128 e4m3) * B(128x16 e4m3) + C.  Lane l holds A row l%16 and B column
+// l%16, 32 consecutive k of the k-group l/16 (any k order works as long as A and
+// B agree).  D: lane l, element r -> row 4*(l/16)+r, column l%16.
+__device__ __forceinline__ v4f mfma16x16x128(const v8i& a, const v8i& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, kWave); }
+__device__ __forceinline__ float shfl_f(float v, int src) { return __shfl(v, src, kWave); }
+__device__ __forceinline__ int shfl_i(int v, int src) { return __shfl(v, src, kWave); }
+
+// OCP e4m3fn byte -> fp32 (exact; v_cvt_f32_fp8).
+__device__ __forceinline__ float e4m3_to_f32(uint32_t byte) {
+  return __builtin_amdgcn_cvt_f32_fp8((int)byte, 0);
+}
+
+// fp32 -> OCP e4m3fn, round to nearest even; |x| must be <= 448 (callers clamp).
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.0f, 0, false) & 0xffu;
+}
+
+// Multi-term e4m3 representation of GEMM2's activations.  With v = x * inv
+// (|v| <= 448 after the per-block scale) the terms are q_0 = e4m3(v) and
+// q_k = e4m3(16^k * (v - sum_{j<k} q_j 16^-j)), so v ~ sum_k q_k 16^-k.  Every
+// residual stays inside the e4m3 range (|residual| <= half an ulp of the
+// previous term) and each term adds ~4 more significant bits: 2 terms ~2^-8,
+// 3 terms ~2^-12, 4 terms ~2^-16 relative error.
+constexpr int kMaxTerms = 4;
+// Output-error budget of one (row, 128-column block) of C: the smallest term
+// count k with 2^(-4k) * ||C_block||_2 * |routing weight| * max|W2 block column|
+// <= kTermTau is used.
+constexpr float kTermTau = 4.0e-3f;
+
+__device__ __forceinline__ void split_terms(float x, float inv, uint32_t (&q)[kMaxTerms]) {
+  float r = fminf(fmaxf(x * inv, -448.0f), 448.0f);
+#pragma unroll
+  for (int k = 0; k < kMaxTerms; k++) {
+    q[k] = f32_to_e4m3(r);
+    r = (r - e4m3_to_f32(q[k])) * 16.0f;
+  }
+}
+
+__device__ __forceinline__ int terms_needed(float gain) {
+  return gain * 0x1p-8f <= kTermTau ? 2 : (gain * 0x1p-12f <= kTermTau ? 3 : 4);
+}
+
+// Term k of the split: A scaled by 2^(-4k) exactly (E8M0 exponent 127 - 4k) in the MFMA itself.
+__device__ __forceinline__ v4f mfma16x16x128_term(const v8i& a, const v8i& b, const v4f& c, int k) {
+  if (k == 0) return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127 - 4 * k, 0, 127);
+}
+
+// Per-block scale of the split: amax -> (inv = 448/amax, scale = amax/448).
+__device__ __forceinline__ void split_scale(float amax, float& inv, float& scale) {
+  if (amax > 0.0f) {
+    inv = __fdiv_rn(448.0f, amax);
+    scale = __fdiv_rn(amax, 448.0f);
+  } else {
+    inv = 0.0f;
+    scale = 0.0f;
+  }
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN -> quiet NaN), as torch's .to(bfloat16).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+__device__ __forceinline__ float half_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Load element i of a routing input of dtype code dt (0 f32, 1 bf16, 2 f16) as fp32.
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
+  if (dt == 0) return reinterpret_cast<const float*>(p)[i];
+  uint16_t h = reinterpret_cast<const uint16_t*>(p)[i];
+  return dt == 1 ? bf16_to_f32(h) : half_to_f32(h);
+}
+
+__device__ __forceinline__ float silu_f32(float x) {
+  return __fdiv_rn(x, 1.0f + __expf(-x));
+}
+
+}  // namespace moefp8

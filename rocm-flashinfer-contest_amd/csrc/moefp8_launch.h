@@ -1,0 +1,64 @@
+// Host-side launchers of the gfx950 MoE kernels (one per kernel family).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moefp8 {
+
+// Routing of every token (main.py:139-165): topk_ids [T,8] ascending, topk_w [T,8].
+void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
+                  int* topk_ids, float* topk_w, hipStream_t stream);
+
+// Stable counting sort of the local (token, expert) pairs (main.py:216-226).
+void launch_permute(const int* topk_ids, const float* topk_w, int T, int E_local, int offset, int tile_m,
+                    int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
+                    int* mtile_offsets, int* info, hipStream_t stream);
+
+// Pointers into the caller's workspace produced by routing + permutation.
+struct Plan {
+  const int* expert_offsets;  // [E_local + 1]
+  const int* perm_token;      // [Pmax]
+  const float* perm_w;        // [Pmax]
+  const int* tok_slot;        // [T * 8]
+  const int* active;          // [E_local]
+  const int* mtile_offsets;   // [E_local + 1]
+  const int* info;            // {P, n_active, m_tiles}
+};
+
+struct Problem {
+  const uint8_t* hidden;  // [T, H]
+  const float* hscale;    // [H/128, T]
+  const uint8_t* w13;     // [E, 2I, H]
+  const float* s13;       // [E, 2I/128, H/128]
+  const uint8_t* w2;      // [E, H, I]
+  const float* s2;        // [E, H/128, I/128]
+  int T, E_local, H, I;
+};
+
+// Small-T path: weight-streaming GEMM1 (+SwiGLU, fp32 C) and GEMM2 (quantise C on load).
+void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* cbuf, int n_slots, hipStream_t stream);
+void launch_gemm2_decode(const Problem& pb, const Plan& pl, const float* cbuf, float* obuf, int n_slots,
+                         hipStream_t stream);
+
+// GEMM1 -> GEMM2 activations of the large-T path: up to kMaxTerms e4m3 planes of C,
+// one fp32 scale per (pair, 128 columns) and the term count of every 16-row sub-tile.
+struct CSplit {
+  uint8_t* q;       // [kMaxTerms][plane] bytes, plane = pmax * I
+  size_t plane;
+  float* scale;     // [pmax][I/128]
+  uint8_t* kmax;    // [max_mtiles][tile_m/16][I/128]
+};
+
+// Large-T path: LDS-staged grouped GEMM1 (+SwiGLU + multi-term split of C) and GEMM2.
+void launch_gemm1_prefill(const Problem& pb, const Plan& pl, int tile_m, const CSplit& cs, int max_mtiles,
+                          hipStream_t stream);
+void launch_gemm2_prefill(const Problem& pb, const Plan& pl, int tile_m, const CSplit& cs, float* obuf,
+                          int max_mtiles, hipStream_t stream);
+
+// out[t] = bf16(sum over t's local pairs in ascending expert order of obuf[pair]) (main.py:240-243).
+void launch_combine(const Plan& pl, const float* obuf, uint16_t* out, int T, int H, hipStream_t stream);
+
+int num_compute_units();
+
+}  // namespace moefp8

@@ -1,0 +1,273 @@
+// DeepSeek-V3 no-aux grouped routing and the deterministic token -> local-expert
+// permutation, for gfx950 wave64.
+//
+// route_kernel   restates solutions/moe_fp8/main.py:139-165 (_route) in the
+//                canonical arithmetic of the oracle: fp64-evaluated sigmoid rounded
+//                once to fp32, (value desc, index asc) ranking for groups and
+//                experts, ascending-id output, sequential fp32 normaliser.
+// permute_kernel restates the selection of main.py:216-226: for each local
+//                expert in ascending order, the tokens that picked it in ascending
+//                token order (torch.nonzero), as one stable counting sort.
+#include "moefp8_device.h"
+#include "moefp8_launch.h"
+
+#pragma clang fp contract(off)
+
+namespace moefp8 {
+
+// Is (va, ia) ranked before (vb, ib)?  Larger value first, lower index on ties.
+__device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// One wavefront per token; lane l owns experts 4l..4l+3, so lanes 8g..8g+7 own group g.
+__global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ logits, int logits_dt,
+                                                    const void* __restrict__ bias, int bias_dt, int64_t T,
+                                                    float rsf, int* __restrict__ topk_ids,
+                                                    float* __restrict__ topk_w) {
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  const int waves_per_block = blockDim.x >> 6;
+  float b[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) b[i] = load_as_f32(bias, bias_dt, 4 * lane + i);
+
+  for (int64_t t = (int64_t)blockIdx.x * waves_per_block + wave; t < T;
+       t += (int64_t)gridDim.x * waves_per_block) {
+    float x[4];
+    if (logits_dt == 0) {
+      const float4 v = reinterpret_cast<const float4*>(logits)[t * (kEGlobal / 4) + lane];
+      x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) x[i] = load_as_f32(logits, logits_dt, t * kEGlobal + 4 * lane + i);
+    }
+    float s[4], sb[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      s[i] = (float)(1.0 / (1.0 + exp(-(double)x[i])));   // main.py:147
+      sb[i] = s[i] + b[i];                                  // main.py:148
+    }
+
+    // per-group sum of the two largest sb (main.py:151-153): lane top-2, then merge over 8 lanes
+    float m1 = fmaxf(sb[0], sb[1]), m2 = fminf(sb[0], sb[1]);
+#pragma unroll
+    for (int i = 2; i < 4; i++) {
+      const float v = sb[i];
+      const float n2 = fmaxf(fminf(m1, v), m2);
+      m1 = fmaxf(m1, v);
+      m2 = n2;
+    }
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+      const float o1 = shfl_xor_f(m1, off), o2 = shfl_xor_f(m2, off);
+      const float n2 = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
+      m1 = fmaxf(m1, o1);
+      m2 = n2;
+    }
+    const float gscore = m1 + m2;
+
+    // top-4 of 8 groups (main.py:154-156)
+    const int my_group = lane >> 3;
+    int beaten_by = 0;
+#pragma unroll
+    for (int g = 0; g < kNGroup; g++) {
+      const float gs = shfl_f(gscore, 8 * g);
+      beaten_by += ranks_before(gs, g, gscore, my_group) ? 1 : 0;
+    }
+    const bool group_kept = beaten_by < kTopKGroup;
+
+    // top-8 experts inside the kept groups (main.py:158-160), one arg-max per round
+    bool alive[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) alive[i] = group_kept;
+    int sel[kTopK];
+#pragma unroll
+    for (int r = 0; r < kTopK; r++) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        if (alive[i] && ranks_before(sb[i], 4 * lane + i, bv, bi)) {
+          bv = sb[i];
+          bi = 4 * lane + i;
+        }
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        const float ov = shfl_xor_f(bv, off);
+        const int oi = shfl_xor_i(bi, off);
+        if (ranks_before(ov, oi, bv, bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      sel[r] = bi;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        if (bi == 4 * lane + i) alive[i] = false;
+    }
+
+    // ascending id order (odd-even transposition network, 8 elements)
+#pragma unroll
+    for (int pass = 0; pass < kTopK; pass++) {
+#pragma unroll
+      for (int j = pass & 1; j + 1 < kTopK; j += 2) {
+        const int lo = min(sel[j], sel[j + 1]), hi = max(sel[j], sel[j + 1]);
+        sel[j] = lo;
+        sel[j + 1] = hi;
+      }
+    }
+
+    // weights from the unbiased s, normalised in ascending id order (main.py:162-164)
+    float s_sel[kTopK];
+#pragma unroll
+    for (int j = 0; j < kTopK; j++) {
+      const int owner = sel[j] >> 2, slot = sel[j] & 3;
+      const float mine = slot == 0 ? s[0] : slot == 1 ? s[1] : slot == 2 ? s[2] : s[3];
+      s_sel[j] = __shfl(mine, owner, kWave);
+    }
+    float acc = s_sel[0];
+#pragma unroll
+    for (int j = 1; j < kTopK; j++) acc = acc + s_sel[j];
+    const float denom = acc + 1e-20f;
+    if (lane < kTopK) {
+      float sv = s_sel[0];
+      int id = sel[0];
+#pragma unroll
+      for (int j = 1; j < kTopK; j++)
+        if (lane == j) {
+          sv = s_sel[j];
+          id = sel[j];
+        }
+      topk_ids[t * kTopK + lane] = id;
+      topk_w[t * kTopK + lane] = __fdiv_rn(sv, denom) * rsf;
+    }
+  }
+}
+
+// Single-workgroup stable counting sort of (token, local expert) pairs.
+//   counts/offsets  per local expert (main.py:222, 225)
+//   perm_token[p]   token of pair p, expert-major, token-ascending
+//   perm_w[p]       routing weight of pair p (main.py:240)
+//   tok_slot[t][k]  pair index of token t's k-th local expert (ascending expert), -1 padded
+//   active[]        local experts with >= 1 token, ascending; info[] totals
+constexpr int kPermThreads = 1024;
+constexpr int kPermWaves = kPermThreads / kWave;
+
+__global__ __launch_bounds__(kPermThreads) void permute_kernel(
+    const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int E_local, int offset,
+    int tile_m, int* __restrict__ expert_offsets, int* __restrict__ perm_token, float* __restrict__ perm_w,
+    int* __restrict__ tok_slot, int* __restrict__ active, int* __restrict__ mtile_offsets,
+    int* __restrict__ info) {
+  __shared__ int cnt[kEGlobal];
+  __shared__ int base[kEGlobal];
+  __shared__ int wcnt[kPermWaves][kEGlobal];
+  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+
+  for (int e = tid; e < E_local; e += kPermThreads) cnt[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < T * kTopK; i += kPermThreads) {
+    const int le = topk_ids[i] - offset;
+    if (le >= 0 && le < E_local) atomicAdd(&cnt[le], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0, n_act = 0, mt = 0;
+    for (int e = 0; e < E_local; e++) {
+      expert_offsets[e] = run;
+      mtile_offsets[e] = mt;
+      base[e] = run;
+      run += cnt[e];
+      mt += (cnt[e] + tile_m - 1) / tile_m;
+      if (cnt[e] > 0) active[n_act++] = e;
+    }
+    expert_offsets[E_local] = run;
+    mtile_offsets[E_local] = mt;
+    info[0] = run;    // P
+    info[1] = n_act;  // active experts
+    info[2] = mt;     // m-tiles of height tile_m
+  }
+  __syncthreads();
+
+  for (int c0 = 0; c0 < T; c0 += kPermThreads) {
+    const int t = c0 + tid;
+    int les[kTopK], slots[kTopK], rank[kTopK];
+    int n = 0;
+    if (t < T) {
+#pragma unroll
+      for (int j = 0; j < kTopK; j++) {
+        const int le = topk_ids[t * kTopK + j] - offset;
+        if (le >= 0 && le < E_local) {
+#pragma unroll
+          for (int k = 0; k < kTopK; k++)
+            if (k == n) {
+              les[k] = le;
+              slots[k] = j;
+            }
+          n++;
+        }
+      }
+    }
+    int ptr = 0;
+    for (int e = 0; e < E_local; e++) {
+      int cur = -1;
+#pragma unroll
+      for (int k = 0; k < kTopK; k++)
+        if (k == ptr) cur = les[k];
+      const bool pick = ptr < n && cur == e;
+      const uint64_t m = __ballot(pick);
+      if (lane == 0) wcnt[wave][e] = __popcll(m);
+      if (pick) {
+        const int r = __popcll(m & ((1ull << lane) - 1ull));
+#pragma unroll
+        for (int k = 0; k < kTopK; k++)
+          if (k == ptr) rank[k] = r;
+        ptr++;
+      }
+    }
+    __syncthreads();
+    for (int e = tid; e < E_local; e += kPermThreads) {
+      int run = base[e];
+      for (int w = 0; w < kPermWaves; w++) {
+        const int c = wcnt[w][e];
+        wcnt[w][e] = run;
+        run += c;
+      }
+      base[e] = run;
+    }
+    __syncthreads();
+    if (t < T) {
+#pragma unroll
+      for (int k = 0; k < kTopK; k++) {
+        int pos = -1;
+        if (k < n) {
+          pos = wcnt[wave][les[k]] + rank[k];
+          perm_token[pos] = t;
+          perm_w[pos] = topk_w[t * kTopK + slots[k]];
+        }
+        tok_slot[t * kTopK + k] = pos;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
+                  int* topk_ids, float* topk_w, hipStream_t stream) {
+  if (T <= 0) return;
+  const int64_t tokens_per_block = 4;
+  int64_t blocks = (T + tokens_per_block - 1) / tokens_per_block;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(route_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, logits, logits_dt, bias,
+                     bias_dt, T, rsf, topk_ids, topk_w);
+}
+
+void launch_permute(const int* topk_ids, const float* topk_w, int T, int E_local, int offset, int tile_m,
+                    int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
+                    int* mtile_offsets, int* info, hipStream_t stream) {
+  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPermThreads), 0, stream, topk_ids, topk_w, T, E_local,
+                     offset, tile_m, expert_offsets, perm_token, perm_w, tok_slot, active, mtile_offsets, info);
+}
+
+}  // namespace moefp8

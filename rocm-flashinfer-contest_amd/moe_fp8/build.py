@@ -1,0 +1,71 @@
+"""Build the gfx950 HIP library ``libmoefp8.so`` in-tree (hipcc, no JIT cache).
+
+    python -m moe_fp8.build        (with rocm-flashinfer-contest_amd/ on sys.path)
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR.parent / "csrc"
+LIB = PKG_DIR / "libmoefp8.so"
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17",
+    # keep the compiler from emitting packed fp32 VALU ops
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise FileNotFoundError("hipcc not found (ROCm toolchain required)")
+
+
+def sources():
+    return sorted(CSRC.glob("*.hip"))
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source for gfx950 and link ``libmoefp8.so`` (always rebuilds)."""
+    cc = hipcc()
+    srcs = sources()
+    with tempfile.TemporaryDirectory(prefix="moefp8_build_") as tmp:
+        objs, procs = [], []
+        for s in srcs:
+            o = Path(tmp) / (s.stem + ".o")
+            cmd = [cc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            procs.append((s, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+            objs.append(str(o))
+        failed = []
+        for s, p in procs:
+            out, _ = p.communicate()
+            text = "\n".join(l for l in out.decode(errors="replace").splitlines() if "packed-fp32-ops" not in l)
+            if p.returncode != 0:
+                failed.append(f"{s.name}:\n{text}")
+            elif verbose and text.strip():
+                print(text)
+        if failed:
+            raise RuntimeError("hipcc failed:\n" + "\n".join(failed))
+        tmp_lib = Path(tmp) / LIB.name
+        cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp_lib), *objs]
+        r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+        if r.returncode != 0:
+            raise RuntimeError("link failed:\n" + r.stdout.decode(errors="replace"))
+        shutil.copyfile(tmp_lib, str(LIB) + ".tmp")
+        os.replace(str(LIB) + ".tmp", LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,121 @@
+"""C-ABI library: builds for gfx950, loads, exports every declared symbol, and rejects
+bad arguments on the host before any GPU work.  CPU only (no kernel is launched)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from moe_fp8 import _abi
+from moe_fp8 import build as mbuild
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "moefp8.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _abi.LIB_PATH.exists():
+        mbuild.build()
+    return _abi.load()
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(moefp8_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_bound_exports():
+    assert declared_functions() == sorted(_abi.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_library_is_built_for_gfx950_only():
+    data = _abi.LIB_PATH.read_bytes()
+    assert b"gfx950" in data
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert other not in data
+
+
+def test_abi_version_and_strerror(lib):
+    assert lib.moefp8_abi_version() == _abi.ABI_VERSION
+    for code in _abi.STATUS:
+        assert lib.moefp8_strerror(code)
+    assert lib.moefp8_strerror(0) == b"ok"
+    assert lib.moefp8_strerror(12345) == b"unknown status"
+
+
+def test_workspace_size(lib):
+    full = _abi.workspace_size(lib, 8192, 32, 7168, 2048)
+    small = _abi.workspace_size(lib, 16, 32, 7168, 2048)
+    assert small < full
+    pmax = 8192 * 8
+    assert full >= pmax * 7168 * 4          # fp32 per-pair GEMM2 rows
+    assert _abi.workspace_size(lib, 0, 32, 7168, 2048) > 0
+    out = ctypes.c_size_t()
+    assert lib.moefp8_workspace_size(16, 32, 7000, 2048, ctypes.byref(out)) == -2   # H not a multiple of 128
+    assert lib.moefp8_workspace_size(16, 0, 7168, 2048, ctypes.byref(out)) == -2
+    assert lib.moefp8_workspace_size(16, 257, 7168, 2048, ctypes.byref(out)) == -2
+    assert lib.moefp8_workspace_size(-1, 32, 7168, 2048, ctypes.byref(out)) == -2
+    assert lib.moefp8_workspace_size(16, 32, 7168, 2048, None) == -1
+
+
+def _args(**kw):
+    a = _abi.MoeFp8Args()
+    a.num_tokens, a.num_local_experts, a.hidden_size, a.intermediate_size = 16, 32, 7168, 2048
+    a.routed_scaling_factor = 2.5
+    for i, f in enumerate(("routing_logits", "routing_bias", "hidden_states", "hidden_states_scale",
+                           "gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale",
+                           "output")):
+        setattr(a, f, 0x100000 * (i + 1))     # fake, aligned, never dereferenced: validation fails first
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_run_rejects_bad_arguments_before_any_launch(lib):
+    ws = 0x7000000
+    run = lambda a, n=1 << 40, w=ws: lib.moefp8_run(ctypes.byref(a), w, n, None)
+    assert lib.moefp8_run(None, ws, 0, None) == -1
+    assert run(_args(hidden_size=100)) == -2
+    assert run(_args(intermediate_size=0)) == -2
+    assert run(_args(num_local_experts=0)) == -2
+    assert run(_args(num_tokens=-5)) == -2
+    assert run(_args(logits_dtype=7)) == -3
+    assert run(_args(bias_dtype=-1)) == -3
+    assert run(_args(routing_logits=None)) == -1
+    assert run(_args(output=None)) == -1
+    assert run(_args(gemm2_weights_scale=None)) == -1
+    assert run(_args(hidden_states=0x100001)) == -4
+    assert run(_args(routing_logits=0x100002)) == -4              # fp32 logits need 16-byte rows
+    assert run(_args(gemm1_weights_scale=0x100002)) == -4
+    assert run(_args(), n=1024) == -5                              # workspace too small
+    assert run(_args(), w=0) == -5
+    assert run(_args(num_tokens=0)) == 0                           # nothing to do, nothing launched
+
+
+def test_route_rejects_bad_arguments(lib):
+    f = lib.moefp8_route
+    assert f(0x1000, 0, 0x2000, 1, -1, 2.5, 0x3000, 0x4000, None) == -2
+    assert f(0x1000, 9, 0x2000, 1, 4, 2.5, 0x3000, 0x4000, None) == -3
+    assert f(None, 0, 0x2000, 1, 4, 2.5, 0x3000, 0x4000, None) == -1
+    assert f(0x1000, 0, 0x2000, 1, 0, 2.5, 0x3000, 0x4000, None) == 0
+
+
+def test_python_entry_point_fails_loudly_without_device_tensors(lib):
+    import torch
+    import moe_fp8
+    with pytest.raises(ValueError):
+        moe_fp8.run(torch.zeros(4, 256), torch.zeros(256), torch.zeros(4, 256, dtype=torch.uint8),
+                    torch.ones(2, 4), torch.zeros(1, 256, 256, dtype=torch.uint8), torch.ones(1, 2, 2),
+                    torch.zeros(1, 256, 128, dtype=torch.uint8), torch.ones(1, 2, 1), 0, 2.5)
+
+
+def test_missing_library_raises(tmp_path):
+    with pytest.raises(FileNotFoundError):
+        _abi.load(tmp_path / "libmoefp8.so")

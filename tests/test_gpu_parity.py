@@ -1,0 +1,218 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle.
+
+Bars: routing ids / weights and the token permutation bit-exact; bf16 output
+within atol 1e-2 / rtol 2e-2 of the oracle's fp32 output on every element.
+"""
+import numpy as np
+import pytest
+import torch
+
+import moe_oracle as O
+import moe_fp8
+from moe_fp8 import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+ATOL, RTOL = 1e-2, 2e-2
+WORKLOADS = W.workloads()
+
+
+def to_dev(args):
+    return tuple(a.to(DEV) if isinstance(a, torch.Tensor) else a for a in args)
+
+
+def to_cpu(args):
+    return tuple(a.cpu() if isinstance(a, torch.Tensor) else a for a in args)
+
+
+def assert_close(out, ref32, label):
+    got = out.float().cpu()
+    err = (got - ref32).abs()
+    bad = err > ATOL + RTOL * ref32.abs()
+    n_bad = int(bad.sum())
+    assert n_bad == 0, (f"{label}: {n_bad} of {got.numel()} elements outside atol {ATOL} / rtol {RTOL}; "
+                        f"max abs err {float(err.max()):.3e}")
+    return float(err.max())
+
+
+def oracle_route(logits, bias, rsf=W.RSF):
+    return O.route(logits.float().cpu().numpy(), bias.float().cpu().numpy(), rsf)
+
+
+def boosted(args, E_local, offset, boost=1.5):
+    """Lean half of the tokens towards the local experts so reduced cases have local work."""
+    logits = args[0].clone()
+    lo, hi = max(offset, 0), min(offset + E_local, 256)
+    if hi > lo:
+        logits[: logits.shape[0] // 2, lo:hi] += boost
+    return (logits,) + tuple(args[1:])
+
+
+# ----------------------------------------------------------------------------- routing
+
+@pytest.mark.parametrize("name", list(WORKLOADS))
+def test_route_bit_exact_on_workloads(name):
+    print(f"[route] {name}", flush=True)
+    logits, bias, _, _ = W.make_activations(WORKLOADS[name], device="cpu", H=128)
+    ids, w = moe_fp8.route(logits.to(DEV), bias.to(DEV), W.RSF)
+    ridx, rw, _, _ = oracle_route(logits, bias)
+    assert np.array_equal(ids.cpu().numpy(), ridx)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
+
+
+@pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("logits_dtype", [torch.float32, torch.bfloat16])
+def test_route_input_dtypes(logits_dtype, bias_dtype):
+    print(f"[route dtypes] {logits_dtype} {bias_dtype}", flush=True)
+    g = torch.Generator().manual_seed(31)
+    logits = torch.randn(333, 256, generator=g).to(logits_dtype)
+    bias = (torch.randn(256, generator=g) * 0.1).to(bias_dtype)
+    ids, w = moe_fp8.route(logits.to(DEV), bias.to(DEV), 1.7)
+    ridx, rw, _, _ = O.route(logits.float().numpy(), bias.float().numpy(), 1.7)
+    assert np.array_equal(ids.cpu().numpy(), ridx)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
+
+
+def test_route_ties_and_extremes():
+    logits = torch.zeros(6, 256)
+    bias = torch.zeros(256)
+    logits[1] = -200.0                             # s underflows to 0 for every expert
+    logits[2] = 200.0                              # s == 1 everywhere
+    logits[3, ::7] = 3.0
+    logits[4] = torch.linspace(-5, 5, 256)
+    logits[5, 100] = float("inf")
+    bias[200:] = 0.5
+    ids, w = moe_fp8.route(logits.to(DEV), bias.to(DEV), 2.5)
+    ridx, rw, _, _ = oracle_route(logits, bias, 2.5)
+    assert np.array_equal(ids.cpu().numpy(), ridx)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
+
+
+def test_route_golden_fixtures():
+    from pathlib import Path
+    for f in sorted((Path(__file__).resolve().parent / "golden").glob("*.npz")):
+        d = np.load(f)
+        bias = torch.from_numpy(d["bias_bf16_bits"].astype(np.int16)).view(torch.bfloat16)
+        ids, w = moe_fp8.route(torch.from_numpy(d["logits"]).to(DEV), bias.to(DEV), float(d["rsf"]))
+        assert np.array_equal(ids.cpu().numpy(), d["topk_ids"]), f.name
+        assert np.array_equal(w.cpu().numpy().view(np.uint32), d["topk_w"].view(np.uint32)), f.name
+
+
+# ----------------------------------------------------------------------------- full path, reduced shapes
+
+REDUCED = [
+    # (T, E_local, H, I, offset)
+    (1, 8, 256, 128, 0),
+    (5, 8, 512, 256, 0),
+    (16, 32, 256, 256, 0),
+    (64, 32, 256, 128, 0),
+    (65, 32, 256, 128, 0),
+    (300, 16, 512, 256, 0),
+    (1000, 32, 384, 256, 0),
+    (777, 8, 256, 128, 252),
+    (200, 32, 256, 128, 224),
+    (100, 4, 256, 128, -2),
+    (50, 32, 256, 128, 300),
+    (2500, 32, 256, 128, 0),
+]
+
+
+@pytest.mark.parametrize("T,E_local,H,I,offset", REDUCED)
+def test_full_path_reduced_shapes(T, E_local, H, I, offset):
+    print(f"[reduced] T={T} E_local={E_local} H={H} I={I} offset={offset}", flush=True)
+    wl = W.Workload(f"r{T}", T, 1000 + T)
+    weights = W.make_weights(E_local, H, I, device="cpu", seed=77 + E_local)
+    args = boosted(W.make_inputs(wl, device="cpu", E_local=E_local, H=H, I=I, weights=weights,
+                                 local_expert_offset=offset), E_local, offset)
+    dbg = {}
+    out = moe_fp8.run(*to_dev(args), debug=dbg)
+    torch.cuda.synchronize()
+    ref32, ref_bf16 = O.moe_forward(*args)
+    ridx, rw, _, _ = oracle_route(args[0], args[1])
+    counts, offsets, ptok, _ = O.permute(ridx, rw, E_local, offset)
+    assert np.array_equal(dbg["topk_ids"].cpu().numpy(), ridx)
+    assert np.array_equal(dbg["topk_weights"].cpu().numpy().view(np.uint32), rw.view(np.uint32))
+    assert np.array_equal(dbg["expert_offsets"].cpu().numpy(), offsets)
+    assert np.array_equal(dbg["permuted_tokens"].cpu().numpy()[: offsets[-1]], ptok)
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (T, H)
+    assert_close(out, ref32, f"T={T} E={E_local} H={H} I={I} off={offset}")
+    # tokens without a local expert are exact zeros
+    nolocal = ~np.any((ridx >= offset) & (ridx < offset + E_local), axis=1)
+    assert torch.all(out.cpu()[torch.from_numpy(nolocal)] == 0)
+
+
+def test_golden_fixtures_full_path():
+    from pathlib import Path
+    for f in sorted((Path(__file__).resolve().parent / "golden").glob("moe_*.npz")):
+        d = np.load(f)
+        bias = torch.from_numpy(d["bias_bf16_bits"].astype(np.int16)).view(torch.bfloat16)
+        args = (torch.from_numpy(d["logits"]), bias, torch.from_numpy(d["hidden"]).view(torch.float8_e4m3fn),
+                torch.from_numpy(d["hidden_scale"]), torch.from_numpy(d["w13"]).view(torch.float8_e4m3fn),
+                torch.from_numpy(d["s13"]), torch.from_numpy(d["w2"]).view(torch.float8_e4m3fn),
+                torch.from_numpy(d["s2"]), int(d["offset"]), float(d["rsf"]))
+        out = moe_fp8.run(*to_dev(args))
+        ref = torch.from_numpy(d["out_fp64"]).float()
+        assert_close(out, ref, f.name)
+
+
+def test_deterministic_and_inputs_untouched():
+    T, E_local, H, I = 700, 32, 256, 128
+    wl = W.Workload("det", T, 5)
+    weights = W.make_weights(E_local, H, I, device="cpu", seed=3)
+    args = to_dev(boosted(W.make_inputs(wl, device="cpu", E_local=E_local, H=H, I=I, weights=weights),
+                          E_local, 0))
+    snap = [a.clone() if isinstance(a, torch.Tensor) else a for a in args]
+    a = moe_fp8.run(*args)
+    b = moe_fp8.run(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    for x, y in zip(args, snap):
+        if isinstance(x, torch.Tensor):
+            assert torch.equal(x.view(torch.uint8) if x.dtype == torch.float8_e4m3fn else x,
+                               y.view(torch.uint8) if y.dtype == torch.float8_e4m3fn else y)
+
+
+def test_zero_tokens_and_tensor_scalars():
+    E_local, H, I = 4, 256, 128
+    weights = W.make_weights(E_local, H, I, device=DEV, seed=9)
+    empty = W.make_inputs(W.Workload("e", 0, 1), device=DEV, E_local=E_local, H=H, I=I, weights=weights)
+    out = moe_fp8.run(*empty)
+    assert tuple(out.shape) == (0, H)
+    args = W.make_inputs(W.Workload("s", 9, 2), device=DEV, E_local=E_local, H=H, I=I, weights=weights)
+    a = moe_fp8.run(*args[:8], torch.tensor(0, device=DEV), torch.tensor(2.5, device=DEV))
+    b = moe_fp8.run(*args)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+# ----------------------------------------------------------------------------- full path, full shapes
+
+@pytest.fixture(scope="module")
+def full_weights():
+    w = W.make_weights(device=DEV)
+    torch.cuda.synchronize()
+    return w, to_cpu(w)
+
+
+@pytest.mark.parametrize("name", list(WORKLOADS))
+def test_full_path_workloads(name, full_weights):
+    """Every named workload at H=7168, I=2048, 32 local experts."""
+    wl = WORKLOADS[name]
+    print(f"[full] {name} T={wl.T}", flush=True)
+    w_dev, w_cpu = full_weights
+    act = W.make_activations(wl, device=DEV)
+    dbg = {}
+    out = moe_fp8.run(*act, *w_dev, 0, W.RSF, debug=dbg)
+    torch.cuda.synchronize()
+    act_cpu = to_cpu(act)
+    ridx, rw, _, _ = oracle_route(act_cpu[0], act_cpu[1])
+    counts, offsets, ptok, _ = O.permute(ridx, rw, 32, 0)
+    assert np.array_equal(dbg["topk_ids"].cpu().numpy(), ridx)
+    assert np.array_equal(dbg["topk_weights"].cpu().numpy().view(np.uint32), rw.view(np.uint32))
+    assert np.array_equal(dbg["expert_offsets"].cpu().numpy(), offsets)
+    assert np.array_equal(dbg["permuted_tokens"].cpu().numpy()[: offsets[-1]], ptok)
+    ref32, _ = O.moe_forward(*act_cpu, *w_cpu, 0, W.RSF)
+    err = assert_close(out, ref32, name)
+    print(f"[full] {name} P={int(counts.sum())} active={int((counts > 0).sum())} max_abs_err={err:.3e}", flush=True)
+    if name == "skewed_t5000":
+        assert counts.min() == 0 and counts.max() > 2000
