@@ -64,6 +64,8 @@ __global__ __launch_bounds__(64 * kDecWaves) void gemm1_decode_kernel(Problem pb
       const int dr = m0 + kg * 4 + r;
       tok_d[r] = pl.perm_token[row0 + (dr < M ? dr : 0)];
     }
+    // exact-product sub-tile if any of its 16 pairs is flagged
+    const bool exact = __ballot(lane < 16 && a_ok && pl.exact[row0 + ar]) != 0;
     v4f acc[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -88,9 +90,18 @@ __global__ __launch_bounds__(64 * kDecWaves) void gemm1_decode_kernel(Problem pb
       for (int u = 0; u < kDec1Unroll; u++) {
         const int kb = kb0 + u * kDecWaves;
         if (kb < KB) {
+          v8h a16[4];
+          if (exact) widen_fp8_operand(a[u], a16);
 #pragma unroll
           for (int j = 0; j < 4; j++) {
-            const v4f p = mfma16x16x128(a[u], b[u][j], v4f{0.f, 0.f, 0.f, 0.f});
+            v4f p;
+            if (exact) {
+              v8h b16[4];
+              widen_fp8_operand(b[u][j], b16);
+              p = mfma_f16_block(a16, b16, v4f{0.f, 0.f, 0.f, 0.f});
+            } else {
+              p = mfma16x16x128(a[u], b[u][j], v4f{0.f, 0.f, 0.f, 0.f});
+            }
             const float sw = j < 2 ? su[u] : sg[u];
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[j][r] += p[r] * (sa[u][r] * sw);
@@ -149,6 +160,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void gemm2_decode_kernel(Problem pb
     const bool a_ok = ar < M;
     const float* crow = cbuf + (size_t)(row0 + (a_ok ? ar : 0)) * I + kg * 32;
     const float w_row = a_ok ? fabsf(pl.perm_w[row0 + ar]) : 0.0f;
+    const bool exact = __ballot(lane < 16 && a_ok && pl.exact[row0 + ar]) != 0;
     v4f acc[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -198,6 +210,30 @@ __global__ __launch_bounds__(64 * kDecWaves) void gemm2_decode_kernel(Problem pb
           for (int off = 1; off < 64; off <<= 1) wm = fmaxf(wm, shfl_xor_f(wm, off));
           float inv, scale;
           split_scale(amax, inv, scale);
+          float sa[4];
+#pragma unroll
+          for (int r = 0; r < 4; r++) sa[r] = shfl_f(scale, kg * 4 + r);
+          if (exact) {
+            // two-term f16 split of C, exact products on the f16 MFMA
+            v8h hi[4], lo[4];
+#pragma unroll
+            for (int i = 0; i < 32; i++) {
+              _Float16 h, l;
+              split_f16(cv[u][i], inv, h, l);
+              hi[i >> 3][i & 7] = h;
+              lo[i >> 3][i & 7] = l;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              v8h b16[4];
+              widen_fp8_operand(b[u][j], b16);
+              v4f p = mfma_f16_block(hi, b16, v4f{0.f, 0.f, 0.f, 0.f});
+              p = mfma_f16_block(lo, b16, p);
+#pragma unroll
+              for (int r = 0; r < 4; r++) acc[j][r] += p[r] * (sa[r] * sw[u]);
+            }
+            continue;
+          }
           int nt = terms_needed(sqrtf(ssq) * w_row * 448.0f * wm);
 #pragma unroll
           for (int off = 1; off < 64; off <<= 1) nt = max(nt, shfl_xor_i(nt, off));
@@ -215,9 +251,6 @@ __global__ __launch_bounds__(64 * kDecWaves) void gemm2_decode_kernel(Problem pb
 #pragma unroll
             for (int k = 0; k < kMaxTerms; k++) aq[k][w4] = (int)packed[k];
           }
-          float sa[4];
-#pragma unroll
-          for (int r = 0; r < 4; r++) sa[r] = shfl_f(scale, kg * 4 + r);
 #pragma unroll
           for (int j = 0; j < 4; j++) {
             v4f p = v4f{0.f, 0.f, 0.f, 0.f};

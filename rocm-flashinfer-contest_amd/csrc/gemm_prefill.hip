@@ -125,6 +125,13 @@ __global__ __launch_bounds__(kPfThreads) void gemm1_prefill_kernel(Problem pb, P
     for (int ms = 0; ms < MS; ms++)
 #pragma unroll
       for (int j = 0; j < 4; j++) acc[ms][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    // exact-product sub-tiles: bit ms set if any of its 16 pairs is flagged
+    uint32_t exact_mask = 0;
+#pragma unroll
+    for (int ms = 0; ms < MS; ms++) {
+      const int r = ms * 16 + lr;
+      if (__ballot(lane < 16 && r < M && pl.exact[row0 + r]) != 0) exact_mask |= 1u << ms;
+    }
 
     // prologue: K block 0 -> LDS stage 0, B block 0 -> registers
     v4i areg[ACH];
@@ -157,6 +164,20 @@ __global__ __launch_bounds__(kPfThreads) void gemm1_prefill_kernel(Problem pb, P
       for (int ms = 0; ms < MS; ms++) {
         const v8i a = lds_a_operand(a_lds[st], ms, lr, kg);
         const v4f sa = *reinterpret_cast<const v4f*>(&sa_lds[st][ms * 16 + kg * 4]);
+        if (exact_mask & (1u << ms)) {
+          v8h a16[4];
+          widen_fp8_operand(a, a16);
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            v8h b16[4];
+            widen_fp8_operand(bcur[j], b16);
+            const v4f p = mfma_f16_block(a16, b16, v4f{0.f, 0.f, 0.f, 0.f});
+            const float sw = j < 2 ? su : sg;
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[ms][j][r] += p[r] * (sa[r] * sw);
+          }
+          continue;
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           const v4f p = mfma16x16x128(a, bcur[j], v4f{0.f, 0.f, 0.f, 0.f});
@@ -226,6 +247,20 @@ __global__ __launch_bounds__(kPfThreads) void gemm1_prefill_kernel(Problem pb, P
         const float wr = row < M ? fabsf(pl.perm_w[row0 + row]) : 0.f;
         kneed[ms] = max(kneed[ms], terms_needed(sqrtf(ss) * wr * wm));
         if (wave == 0 && lr == 0 && row < M) cs.scale[(size_t)(row0 + row) * NT + tc.nt] = scale;
+        if (exact_mask & (1u << ms)) {
+          // exact-product sub-tile: two-term f16 split straight to global
+          if (row < M) {
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+              _Float16 h, l;
+              split_f16(cval[ms][q][r], inv, h, l);
+              const size_t g = (size_t)(row0 + row) * I + n0 + wave * 32 + q * 16 + lr;
+              cs.c16[g] = h;
+              cs.c16[cs.plane + g] = l;
+            }
+          }
+          continue;
+        }
 #pragma unroll
         for (int q = 0; q < 2; q++) {
           uint32_t qv[kMaxTerms];
@@ -238,6 +273,7 @@ __global__ __launch_bounds__(kPfThreads) void gemm1_prefill_kernel(Problem pb, P
       }
       kneed[ms] = max(kneed[ms], shfl_xor_i(kneed[ms], 16));
       kneed[ms] = max(kneed[ms], shfl_xor_i(kneed[ms], 32));
+      if (exact_mask & (1u << ms)) kneed[ms] = kExactTerms;
     }
     if (tid == 0) {
 #pragma unroll
@@ -251,7 +287,7 @@ __global__ __launch_bounds__(kPfThreads) void gemm1_prefill_kernel(Problem pb, P
       const int r = ch >> 3, c = ch & 7;
       if (r < M) {
         const size_t g = (size_t)(row0 + r) * I + n0 + c * 16;
-        const int nk = kmax_lds[r >> 4];
+        const int nk = kmax_lds[r >> 4] == kExactTerms ? 0 : kmax_lds[r >> 4];
 #pragma unroll
         for (int k = 0; k < kMaxTerms; k++)
           if (k < nk) *reinterpret_cast<v4i*>(cs.q + (size_t)k * cs.plane + g) =
@@ -287,7 +323,10 @@ __global__ __launch_bounds__(kPfThreads) void gemm2_prefill_kernel(Problem pb, P
     auto planes_for = [&](int kb) {
       int n = 0;
 #pragma unroll
-      for (int ms = 0; ms < MS; ms++) n = max(n, (int)kmax[ms * KB + kb]);
+      for (int ms = 0; ms < MS; ms++) {
+        const int k = kmax[ms * KB + kb];
+        n = max(n, k == kExactTerms ? 0 : k);
+      }
       return n;
     };
 
@@ -360,6 +399,27 @@ __global__ __launch_bounds__(kPfThreads) void gemm2_prefill_kernel(Problem pb, P
 #pragma unroll
       for (int ms = 0; ms < MS; ms++) {
         const int nk = kmax[ms * KB + kb];
+        const v4f sa_x = *reinterpret_cast<const v4f*>(&sa_lds[st][ms * 16 + kg * 4]);
+        if (nk == kExactTerms) {
+          // exact-product sub-tile: f16 hi/lo split of C from global, W2 widened to f16
+          const size_t g = (size_t)(row0 + min(ms * 16 + lr, M - 1)) * I + kb * kBlock + kg * 32;
+          v8h ah[4], al[4];
+#pragma unroll
+          for (int s4 = 0; s4 < 4; s4++) {
+            ah[s4] = *reinterpret_cast<const v8h*>(cs.c16 + g + 8 * s4);
+            al[s4] = *reinterpret_cast<const v8h*>(cs.c16 + cs.plane + g + 8 * s4);
+          }
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            v8h b16[4];
+            widen_fp8_operand(bcur[j], b16);
+            v4f p = mfma_f16_block(ah, b16, v4f{0.f, 0.f, 0.f, 0.f});
+            p = mfma_f16_block(al, b16, p);
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[ms][j][r] += p[r] * (sa_x[r] * sw);
+          }
+          continue;
+        }
         v8i aq[kMaxTerms];
 #pragma unroll
         for (int k = 0; k < kMaxTerms; k++)

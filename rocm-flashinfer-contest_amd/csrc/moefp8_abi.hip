@@ -26,6 +26,7 @@ int tile_m_for(int64_t T) {
 
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
+  size_t tok_a2, esig, perm_exact, c16;
   size_t cbuf, c_q, c_plane, c_scale, c_kmax, obuf, total;
   int64_t pmax, max_mtiles;
 };
@@ -51,6 +52,9 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.perm_token = take((size_t)pmax * 4);
   L.perm_w = take((size_t)pmax * 4);
   L.tok_slot = take((size_t)T * kTopK * 4);
+  L.tok_a2 = take((size_t)T * 4);
+  L.esig = take((size_t)E_local * 2 * 4);
+  L.perm_exact = take((size_t)pmax);
   // C between the GEMMs: fp32 [pmax, I] (small T) or, for large T, kMaxTerms e4m3 planes
   // [pmax, I] + fp32 scales [pmax, I/128] + per-sub-tile term counts
   const int tm = tile_m_for(T);
@@ -64,6 +68,7 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.c_q = L.cbuf;
   L.c_scale = L.c_q + L.c_plane * kMaxTerms;
   L.c_kmax = L.c_scale + c_scale_bytes;
+  L.c16 = take(L.c_plane * 2 * 2);
   L.obuf = take((size_t)pmax * H * 4);
   L.total = o;
   return L;
@@ -155,7 +160,7 @@ int moefp8_route(const void* routing_logits, int32_t logits_dtype, const void* r
   if (query_device(&dev)) return MOEFP8_ERR_DEVICE;
   hipStream_t s = (hipStream_t)stream;
   launch_route(routing_logits, logits_dtype, routing_bias, bias_dtype, num_tokens, routed_scaling_factor, topk_ids,
-               topk_weights, s);
+               topk_weights, nullptr, s);
   return hipGetLastError() == hipSuccess ? MOEFP8_OK : MOEFP8_ERR_LAUNCH;
 }
 
@@ -195,6 +200,9 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pl.active = reinterpret_cast<int*>(ws + L.active);
   pl.mtile_offsets = reinterpret_cast<int*>(ws + L.mtile_offsets);
   pl.info = reinterpret_cast<int*>(ws + L.info);
+  pl.exact = ws + L.perm_exact;
+  float* tok_a2 = reinterpret_cast<float*>(ws + L.tok_a2);
+  float* esig = reinterpret_cast<float*>(ws + L.esig);
 
   Problem pb;
   pb.hidden = a->hidden_states;
@@ -214,13 +222,15 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
     if (ev) (void)hipEventRecord(ev[i], s);
   };
   mark(0);
+  MagInputs mag = {a->hidden_states, a->hidden_states_scale, a->gemm1_weights_scale, a->gemm2_weights_scale,
+                   H, I, E_local, tok_a2, esig};
   launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,
-               topk_ids, topk_w, s);
+               topk_ids, topk_w, &mag, s);
   mark(1);
   launch_permute(topk_ids, topk_w, (int)T, E_local, a->local_expert_offset, tile_m,
                  const_cast<int*>(pl.expert_offsets), const_cast<int*>(pl.perm_token), const_cast<float*>(pl.perm_w),
                  const_cast<int*>(pl.tok_slot), const_cast<int*>(pl.active), const_cast<int*>(pl.mtile_offsets),
-                 const_cast<int*>(pl.info), s);
+                 const_cast<int*>(pl.info), tok_a2, esig, I, const_cast<uint8_t*>(pl.exact), s);
   mark(2);
   float* obuf = reinterpret_cast<float*>(ws + L.obuf);
   if (T <= kDecodeMaxT) {
@@ -235,6 +245,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
     cs.plane = L.c_plane;
     cs.scale = reinterpret_cast<float*>(ws + L.c_scale);
     cs.kmax = ws + L.c_kmax;
+    cs.c16 = reinterpret_cast<_Float16*>(ws + L.c16);
     launch_gemm1_prefill(pb, pl, tile_m, cs, (int)L.max_mtiles, s);
     mark(3);
     launch_gemm2_prefill(pb, pl, tile_m, cs, obuf, (int)L.max_mtiles, s);

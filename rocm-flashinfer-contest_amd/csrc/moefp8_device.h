@@ -18,12 +18,61 @@ constexpr int kWave = 64;
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 // D = A(16x128 e4m3) * B(128x16 e4m3) + C.  Lane l holds A row l%16 and B column
 // l%16, 32 consecutive k of the k-group l/16 (any k order works as long as A and
 // B agree).  D: lane l, element r -> row 4*(l/16)+r, column l%16.
 __device__ __forceinline__ v4f mfma16x16x128(const v8i& a, const v8i& b, const v4f& c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// Exact-product path.  The fp8 MFMA sums its 128 products with a truncating
+// adder (measured on gfx950: mean error 2^-19.4 of sum|products|, worst 2.4e-5),
+// while the f16 MFMA sums e4m3 products (exact in f16) with fp32-exact accuracy
+// (2^-32).  Sub-tiles whose outputs are large enough for the fp8 error to show
+// against the operator's absolute tolerance run on the f16 MFMA: the same fp8
+// operand registers are widened to f16 (e4m3 -> f16 is exact) and one 128-K
+// block becomes four chained v_mfma_f32_16x16x32_f16.  k-values stay in the
+// same lane/slot order, so A and B still agree on k.
+__device__ __forceinline__ void widen_fp8_operand(const v8i& x, v8h (&y)[4]) {
+#pragma unroll
+  for (int s = 0; s < 4; s++) {
+#pragma unroll
+    for (int w = 0; w < 2; w++) {
+      const uint32_t word = (uint32_t)x[2 * s + w];
+      const v2h lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.0f, false);
+      const v2h hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.0f, true);
+      y[s][4 * w + 0] = lo[0];
+      y[s][4 * w + 1] = lo[1];
+      y[s][4 * w + 2] = hi[0];
+      y[s][4 * w + 3] = hi[1];
+    }
+  }
+}
+
+__device__ __forceinline__ v4f mfma_f16_block(const v8h (&a)[4], const v8h (&b)[4], v4f c) {
+#pragma unroll
+  for (int s = 0; s < 4; s++) c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s], b[s], c, 0, 0, 0);
+  return c;
+}
+
+// Two-term f16 split of v = x * inv (|v| <= 448): v ~ hi + lo, ~2^-22 relative.
+__device__ __forceinline__ void split_f16(float x, float inv, _Float16& hi, _Float16& lo) {
+  const float v = fminf(fmaxf(x * inv, -448.0f), 448.0f);
+  hi = (_Float16)v;
+  lo = (_Float16)(v - (float)hi);
+}
+
+// Predicted size of a pair's output row (rms of routing-weighted GEMM2 output) from
+// the token's squared hidden-state norm and the expert's weight-magnitude estimates;
+// pairs above kPreciseRms run the exact-product path.  rms(G1) ~ ||A|| s13,
+// rms(C) ~ 0.7 rms(G1)^2, rms(O) ~ rms(C) s2 sqrt(I).
+constexpr float kPreciseRms = 96.0f;
+
+__device__ __forceinline__ bool needs_exact_products(float a2, float w, float s13, float s2, float sqrt_i) {
+  return fabsf(w) * 0.7f * a2 * s13 * s13 * s2 * sqrt_i > kPreciseRms;
 }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }

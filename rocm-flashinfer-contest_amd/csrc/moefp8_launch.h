@@ -6,14 +6,28 @@
 
 namespace moefp8 {
 
-// Routing of every token (main.py:139-165): topk_ids [T,8] ascending, topk_w [T,8].
-void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
-                  int* topk_ids, float* topk_w, hipStream_t stream);
+// Inputs and outputs of the magnitude estimates behind the exact-product decision.
+struct MagInputs {
+  const uint8_t* hidden;
+  const float* hscale;
+  const float* s13;
+  const float* s2;
+  int H, I, E_local;
+  float* tok_a2;   // [T]   squared norm of each dequantised hidden row
+  float* esig;     // [E, 2] rms estimates of W13 and W2 entries
+};
 
-// Stable counting sort of the local (token, expert) pairs (main.py:216-226).
+// Routing of every token (main.py:139-165): topk_ids [T,8] ascending, topk_w [T,8];
+// with `mag`, also the magnitude estimates.
+void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
+                  int* topk_ids, float* topk_w, const MagInputs* mag, hipStream_t stream);
+
+// Stable counting sort of the local (token, expert) pairs (main.py:216-226), plus the
+// per-pair exact-product flag.
 void launch_permute(const int* topk_ids, const float* topk_w, int T, int E_local, int offset, int tile_m,
                     int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
-                    int* mtile_offsets, int* info, hipStream_t stream);
+                    int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
+                    uint8_t* perm_exact, hipStream_t stream);
 
 // Pointers into the caller's workspace produced by routing + permutation.
 struct Plan {
@@ -24,6 +38,7 @@ struct Plan {
   const int* active;          // [E_local]
   const int* mtile_offsets;   // [E_local + 1]
   const int* info;            // {P, n_active, m_tiles}
+  const uint8_t* exact;       // [Pmax] 1 = pair runs on the exact-product (f16 MFMA) path
 };
 
 struct Problem {
@@ -47,8 +62,12 @@ struct CSplit {
   uint8_t* q;       // [kMaxTerms][plane] bytes, plane = pmax * I
   size_t plane;
   float* scale;     // [pmax][I/128]
-  uint8_t* kmax;    // [max_mtiles][tile_m/16][I/128]
+  uint8_t* kmax;    // [max_mtiles][tile_m/16][I/128]: e4m3 term count, or kExactTerms
+  _Float16* c16;    // [2][pmax][I] two-term f16 split of C for exact-product sub-tiles
 };
+
+// kmax marker of a sub-tile that runs GEMM2 on the exact-product path.
+constexpr int kExactTerms = 16;
 
 // Large-T path: LDS-staged grouped GEMM1 (+SwiGLU + multi-term split of C) and GEMM2.
 void launch_gemm1_prefill(const Problem& pb, const Plan& pl, int tile_m, const CSplit& cs, int max_mtiles,

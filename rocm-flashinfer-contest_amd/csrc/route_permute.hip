@@ -20,11 +20,56 @@ __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib)
   return va > vb || (va == vb && ia < ib);
 }
 
+// Magnitude inputs of the exact-product decision (optional): per token the squared
+// L2 norm of its dequantised hidden row, per local expert an rms estimate of its
+// W13 and W2 entries (448 * largest block scale / 3).
+struct MagArgs {
+  const uint8_t* hidden;   // [T, H] e4m3; NULL = skip
+  const float* hscale;     // [H/128, T]
+  const float* s13;        // [E, 2I/128, H/128]
+  const float* s2;         // [E, H/128, I/128]
+  int H, I, E_local;
+  float* tok_a2;           // [T]
+  float* esig;             // [E, 2]
+};
+
+__device__ void expert_sigma_block(const MagArgs& mg, int e) {
+  __shared__ float red[2][4];
+  const int n13 = (2 * mg.I / kBlock) * (mg.H / kBlock), n2 = (mg.H / kBlock) * (mg.I / kBlock);
+  float m13 = 0.f, m2 = 0.f;
+  for (int i = threadIdx.x; i < n13; i += blockDim.x) m13 = fmaxf(m13, mg.s13[(size_t)e * n13 + i]);
+  for (int i = threadIdx.x; i < n2; i += blockDim.x) m2 = fmaxf(m2, mg.s2[(size_t)e * n2 + i]);
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    m13 = fmaxf(m13, shfl_xor_f(m13, off));
+    m2 = fmaxf(m2, shfl_xor_f(m2, off));
+  }
+  const int wave = threadIdx.x >> 6;
+  if (lane_id() == 0) {
+    red[0][wave] = m13;
+    red[1][wave] = m2;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float a = red[0][0], b = red[1][0];
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++) {
+      a = fmaxf(a, red[0][w]);
+      b = fmaxf(b, red[1][w]);
+    }
+    mg.esig[2 * e] = a * (448.0f / 3.0f);
+    mg.esig[2 * e + 1] = b * (448.0f / 3.0f);
+  }
+}
+
 // One wavefront per token; lane l owns experts 4l..4l+3, so lanes 8g..8g+7 own group g.
 __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ logits, int logits_dt,
                                                     const void* __restrict__ bias, int bias_dt, int64_t T,
                                                     float rsf, int* __restrict__ topk_ids,
-                                                    float* __restrict__ topk_w) {
+                                                    float* __restrict__ topk_w, int token_blocks, MagArgs mg) {
+  if ((int)blockIdx.x >= token_blocks) {                 // trailing blocks: one per local expert
+    expert_sigma_block(mg, blockIdx.x - token_blocks);
+    return;
+  }
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
   const int waves_per_block = blockDim.x >> 6;
@@ -33,7 +78,28 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
   for (int i = 0; i < 4; i++) b[i] = load_as_f32(bias, bias_dt, 4 * lane + i);
 
   for (int64_t t = (int64_t)blockIdx.x * waves_per_block + wave; t < T;
-       t += (int64_t)gridDim.x * waves_per_block) {
+       t += (int64_t)token_blocks * waves_per_block) {
+    if (mg.hidden) {
+      // ||A_t||^2 = sum_kb scale[kb,t]^2 * sum_{k in kb} e4m3(hs[t,k])^2
+      float a2 = 0.f;
+      const uint8_t* row = mg.hidden + t * mg.H;
+      for (int c = lane; c < mg.H / 16; c += kWave) {
+        const v4i q = *reinterpret_cast<const v4i*>(row + c * 16);
+        float ss = 0.f;
+#pragma unroll
+        for (int w4 = 0; w4 < 4; w4++)
+#pragma unroll
+          for (int bb = 0; bb < 4; bb++) {
+            const float v = e4m3_to_f32(((uint32_t)q[w4] >> (8 * bb)) & 0xffu);
+            ss += v * v;
+          }
+        const float sc = mg.hscale[(size_t)(c >> 3) * T + t];
+        a2 += ss * sc * sc;
+      }
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) a2 += shfl_xor_f(a2, off);
+      if (lane == 0) mg.tok_a2[t] = a2;
+    }
     float x[4];
     if (logits_dt == 0) {
       const float4 v = reinterpret_cast<const float4*>(logits)[t * (kEGlobal / 4) + lane];
@@ -159,7 +225,8 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int E_local, int offset,
     int tile_m, int* __restrict__ expert_offsets, int* __restrict__ perm_token, float* __restrict__ perm_w,
     int* __restrict__ tok_slot, int* __restrict__ active, int* __restrict__ mtile_offsets,
-    int* __restrict__ info) {
+    int* __restrict__ info, const float* __restrict__ tok_a2, const float* __restrict__ esig, float sqrt_i,
+    uint8_t* __restrict__ perm_exact) {
   __shared__ int cnt[kEGlobal];
   __shared__ int base[kEGlobal];
   __shared__ int wcnt[kPermWaves][kEGlobal];
@@ -243,8 +310,10 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
         int pos = -1;
         if (k < n) {
           pos = wcnt[wave][les[k]] + rank[k];
+          const float w = topk_w[t * kTopK + slots[k]];
           perm_token[pos] = t;
-          perm_w[pos] = topk_w[t * kTopK + slots[k]];
+          perm_w[pos] = w;
+          perm_exact[pos] = needs_exact_products(tok_a2[t], w, esig[2 * les[k]], esig[2 * les[k] + 1], sqrt_i);
         }
         tok_slot[t * kTopK + k] = pos;
       }
@@ -254,20 +323,36 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
 }
 
 void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
-                  int* topk_ids, float* topk_w, hipStream_t stream) {
+                  int* topk_ids, float* topk_w, const MagInputs* mag, hipStream_t stream) {
   if (T <= 0) return;
   const int64_t tokens_per_block = 4;
   int64_t blocks = (T + tokens_per_block - 1) / tokens_per_block;
   if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(route_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, logits, logits_dt, bias,
-                     bias_dt, T, rsf, topk_ids, topk_w);
+  MagArgs mg = {};
+  int extra = 0;
+  if (mag) {
+    mg.hidden = mag->hidden;
+    mg.hscale = mag->hscale;
+    mg.s13 = mag->s13;
+    mg.s2 = mag->s2;
+    mg.H = mag->H;
+    mg.I = mag->I;
+    mg.E_local = mag->E_local;
+    mg.tok_a2 = mag->tok_a2;
+    mg.esig = mag->esig;
+    extra = mag->E_local;
+  }
+  hipLaunchKernelGGL(route_kernel, dim3((unsigned)(blocks + extra)), dim3(256), 0, stream, logits, logits_dt,
+                     bias, bias_dt, T, rsf, topk_ids, topk_w, (int)blocks, mg);
 }
 
 void launch_permute(const int* topk_ids, const float* topk_w, int T, int E_local, int offset, int tile_m,
                     int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
-                    int* mtile_offsets, int* info, hipStream_t stream) {
+                    int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
+                    uint8_t* perm_exact, hipStream_t stream) {
   hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPermThreads), 0, stream, topk_ids, topk_w, T, E_local,
-                     offset, tile_m, expert_offsets, perm_token, perm_w, tok_slot, active, mtile_offsets, info);
+                     offset, tile_m, expert_offsets, perm_token, perm_w, tok_slot, active, mtile_offsets, info,
+                     tok_a2, esig, sqrtf((float)I), perm_exact);
 }
 
 }  // namespace moefp8

@@ -142,6 +142,27 @@ def test_full_path_reduced_shapes(T, E_local, H, I, offset):
     assert torch.all(out.cpu()[torch.from_numpy(nolocal)] == 0)
 
 
+@pytest.mark.parametrize("T,E_local,H,I", [(16, 8, 512, 256), (64, 32, 256, 256), (300, 16, 512, 256),
+                                              (1500, 32, 256, 128)])
+def test_full_path_high_magnitude_tokens(T, E_local, H, I):
+    """Tokens with 30-120x hidden amplitude (outputs up to ~1e4) take the exact-product
+    sub-tile path; every element must still meet atol 1e-2 / rtol 2e-2."""
+    print(f"[magnitude] T={T} E_local={E_local} H={H} I={I}", flush=True)
+    wl = W.Workload(f"m{T}", T, 2000 + T)
+    weights = W.make_weights(E_local, H, I, device="cpu", seed=5 + E_local)
+    args = boosted(W.make_inputs(wl, device="cpu", E_local=E_local, H=H, I=I, weights=weights), E_local, 0)
+    hss = args[3].clone()
+    amp = torch.ones(T)
+    amp[::7] = torch.linspace(30.0, 120.0, len(amp[::7]))
+    hss *= amp[None, :]
+    args = args[:3] + (hss,) + args[4:]
+    out = moe_fp8.run(*to_dev(args))
+    torch.cuda.synchronize()
+    ref32, _ = O.moe_forward(*args)
+    assert float(ref32.abs().max()) > 500.0
+    assert_close(out, ref32, f"magnitude T={T}")
+
+
 def test_golden_fixtures_full_path():
     from pathlib import Path
     for f in sorted((Path(__file__).resolve().parent / "golden").glob("moe_*.npz")):
