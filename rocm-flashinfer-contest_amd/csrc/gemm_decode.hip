@@ -7,10 +7,8 @@
 // MFMA operand registers; the only LDS use is the fixed-order cross-wave sum.
 //
 // GEMM1  G1 = A_e W13_e^T, C = silu(G1[:, I:]) * G1[:, :I]   (main.py:229-233), C in fp32.
-// GEMM2  O = C W2_e^T, times the pair's routing weight        (main.py:234-241, before
-//        the index_add_).  C is split on load into 2-4 e4m3 terms per 128-block
-//        with one fp32 scale; the term count per 16-row sub-tile follows the
-//        output-error budget of split_terms / terms_needed.
+// GEMM2  O = C W2_e^T times the pair's routing weight, summed per token in ascending
+//        expert order and written as bf16 (main.py:234-243); see gemm2_decode_kernel.
 #include "moefp8_device.h"
 #include "moefp8_launch.h"
 
@@ -18,9 +16,7 @@ namespace moefp8 {
 
 constexpr int kDecWaves = 8;             // waves per workgroup (split K)
 constexpr int kDec1Cols = 32;            // C columns per GEMM1 workgroup (32 up + 32 gate rows of W13)
-constexpr int kDec2Cols = 64;            // H columns per GEMM2 workgroup
 constexpr int kDec1Unroll = 2;           // GEMM1 K blocks in flight per wave
-constexpr int kDec2Unroll = 1;           // GEMM2 K blocks in flight per wave (fp32 C + 4 term planes per block)
 
 __device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
   const v4i* q = reinterpret_cast<const v4i*>(p);
@@ -131,18 +127,24 @@ __global__ __launch_bounds__(64 * kDecWaves) void gemm1_decode_kernel(Problem pb
   }
 }
 
+// GEMM2 for small T (main.py:234-241).  Workgroup = (active expert, 64 H
+// columns); its 8 waves split K and a fixed-order LDS sum gives O for each of the expert's
+// pairs, stored routing-weighted in fp32.  C (fp32 from GEMM1) is split on load into two f16
+// terms per 128-block with one fp32 scale and multiplied with W2 widened to f16: exact
+// products, ~2^-22 relative error on C.  The combine kernel then sums each token's pair rows.
 __global__ __launch_bounds__(64 * kDecWaves) void gemm2_decode_kernel(Problem pb, Plan pl,
-                                                                      const float* __restrict__ cbuf,
-                                                                      float* __restrict__ obuf) {
+                                                                              const float* __restrict__ cbuf,
+                                                                              float* __restrict__ obuf) {
   const int slot = blockIdx.y;
-  if (slot >= pl.info[1]) return;
+  const int n_act = pl.info[1];
+  const int H = pb.H, I = pb.I, T = pb.T;
+  const int h0 = blockIdx.x * kDec2Cols;
+  if (slot >= n_act) return;
   const int e = pl.active[slot];
   const int row0 = pl.expert_offsets[e];
   const int M = pl.expert_offsets[e + 1] - row0;
-  const int H = pb.H, I = pb.I;
   const int KB = I / kBlock;
   const int HB = H / kBlock;
-  const int h0 = blockIdx.x * kDec2Cols;
   const int lane = lane_id(), wave = threadIdx.x >> 6;
   const int lr = lane & 15, kg = lane >> 4;
 
@@ -150,8 +152,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void gemm2_decode_kernel(Problem pb
   const uint8_t* brow[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) brow[j] = wexp + (size_t)(h0 + 16 * j + lr) * I + kg * 32;
-  const float* s2e = pb.s2 + (size_t)e * HB * KB;
-  const float* s_row = s2e + (size_t)(h0 / kBlock) * KB;
+  const float* s_row = pb.s2 + ((size_t)e * HB + h0 / kBlock) * KB;
 
   __shared__ float red[kDecWaves][4][4][64];
 
@@ -159,117 +160,71 @@ __global__ __launch_bounds__(64 * kDecWaves) void gemm2_decode_kernel(Problem pb
     const int ar = m0 + lr;
     const bool a_ok = ar < M;
     const float* crow = cbuf + (size_t)(row0 + (a_ok ? ar : 0)) * I + kg * 32;
-    const float w_row = a_ok ? fabsf(pl.perm_w[row0 + ar]) : 0.0f;
-    const bool exact = __ballot(lane < 16 && a_ok && pl.exact[row0 + ar]) != 0;
     v4f acc[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    for (int kb0 = wave; kb0 < KB; kb0 += kDecWaves * kDec2Unroll) {
-      v8i b[kDec2Unroll][4];
-      float cv[kDec2Unroll][32];
-      float sw[kDec2Unroll], wmax[kDec2Unroll];
+    for (int kb0 = wave; kb0 < KB; kb0 += 2 * kDecWaves) {
+      v8i b[2][4];
+      float cv[2][32];
+      float sw[2];
 #pragma unroll
-      for (int u = 0; u < kDec2Unroll; u++) {
+      for (int u = 0; u < 2; u++) {
         const int kb = kb0 + u * kDecWaves;
         if (kb < KB) {
 #pragma unroll
           for (int j = 0; j < 4; j++) b[u][j] = load_v8i(brow[j] + kb * kBlock);
           const float4* cp = reinterpret_cast<const float4*>(crow + kb * kBlock);
 #pragma unroll
-          for (int q = 0; q < 8; q++) {
-            const float4 v = a_ok ? cp[q] : float4{0.f, 0.f, 0.f, 0.f};
-            cv[u][4 * q + 0] = v.x;
-            cv[u][4 * q + 1] = v.y;
-            cv[u][4 * q + 2] = v.z;
-            cv[u][4 * q + 3] = v.w;
+          for (int c4 = 0; c4 < 8; c4++) {
+            const float4 v = a_ok ? cp[c4] : float4{0.f, 0.f, 0.f, 0.f};
+            cv[u][4 * c4 + 0] = v.x;
+            cv[u][4 * c4 + 1] = v.y;
+            cv[u][4 * c4 + 2] = v.z;
+            cv[u][4 * c4 + 3] = v.w;
           }
           sw[u] = s_row[kb];
-          // largest |W2| this K block can hold: 448 * max over H blocks of its scale
-          float m = 0.f;
-          for (int hb = lane; hb < HB; hb += kWave) m = fmaxf(m, s2e[(size_t)hb * KB + kb]);
-          wmax[u] = m;
         }
       }
 #pragma unroll
-      for (int u = 0; u < kDec2Unroll; u++) {
+      for (int u = 0; u < 2; u++) {
         const int kb = kb0 + u * kDecWaves;
         if (kb < KB) {
-          float amax = 0.f, ssq = 0.f, wm = wmax[u];
+          float amax = 0.f;
 #pragma unroll
-          for (int i = 0; i < 32; i++) {
-            amax = fmaxf(amax, fabsf(cv[u][i]));
-            ssq += cv[u][i] * cv[u][i];
-          }
-#pragma unroll
-          for (int off = 16; off < 64; off <<= 1) {
-            amax = fmaxf(amax, shfl_xor_f(amax, off));
-            ssq += shfl_xor_f(ssq, off);
-          }
-#pragma unroll
-          for (int off = 1; off < 64; off <<= 1) wm = fmaxf(wm, shfl_xor_f(wm, off));
+          for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(cv[u][i]));
+          amax = fmaxf(amax, shfl_xor_f(amax, 16));
+          amax = fmaxf(amax, shfl_xor_f(amax, 32));
           float inv, scale;
           split_scale(amax, inv, scale);
           float sa[4];
 #pragma unroll
           for (int r = 0; r < 4; r++) sa[r] = shfl_f(scale, kg * 4 + r);
-          if (exact) {
-            // two-term f16 split of C, exact products on the f16 MFMA
-            v8h hi[4], lo[4];
+          v8h ch[4], cl[4];
 #pragma unroll
-            for (int i = 0; i < 32; i++) {
-              _Float16 h, l;
-              split_f16(cv[u][i], inv, h, l);
-              hi[i >> 3][i & 7] = h;
-              lo[i >> 3][i & 7] = l;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-              v8h b16[4];
-              widen_fp8_operand(b[u][j], b16);
-              v4f p = mfma_f16_block(hi, b16, v4f{0.f, 0.f, 0.f, 0.f});
-              p = mfma_f16_block(lo, b16, p);
-#pragma unroll
-              for (int r = 0; r < 4; r++) acc[j][r] += p[r] * (sa[r] * sw[u]);
-            }
-            continue;
-          }
-          int nt = terms_needed(sqrtf(ssq) * w_row * 448.0f * wm);
-#pragma unroll
-          for (int off = 1; off < 64; off <<= 1) nt = max(nt, shfl_xor_i(nt, off));
-          v8i aq[kMaxTerms];
-#pragma unroll
-          for (int w4 = 0; w4 < 8; w4++) {
-            uint32_t packed[kMaxTerms] = {0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int bidx = 0; bidx < 4; bidx++) {
-              uint32_t q[kMaxTerms];
-              split_terms(cv[u][4 * w4 + bidx], inv, q);
-#pragma unroll
-              for (int k = 0; k < kMaxTerms; k++) packed[k] |= q[k] << (8 * bidx);
-            }
-#pragma unroll
-            for (int k = 0; k < kMaxTerms; k++) aq[k][w4] = (int)packed[k];
+          for (int i = 0; i < 32; i++) {
+            _Float16 hv, lv;
+            split_f16(cv[u][i], inv, hv, lv);
+            ch[i >> 3][i & 7] = hv;
+            cl[i >> 3][i & 7] = lv;
           }
 #pragma unroll
           for (int j = 0; j < 4; j++) {
-            v4f p = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int k = 0; k < kMaxTerms; k++)
-              if (k < nt) p = mfma16x16x128_term(aq[k], b[u][j], p, k);
+            v8h b16[4];
+            widen_fp8_operand(b[u][j], b16);
+            v4f p = mfma_f16_block(ch, b16, v4f{0.f, 0.f, 0.f, 0.f});
+            p = mfma_f16_block(cl, b16, p);
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[j][r] += p[r] * (sa[r] * sw[u]);
           }
         }
       }
     }
-
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) red[wave][j][r][lane] = acc[j][r];
     __syncthreads();
-    // 16 rows x 64 H columns
     for (int idx = threadIdx.x; idx < 16 * kDec2Cols; idx += 64 * kDecWaves) {
       const int ln = idx & 63, j = (idx >> 6) & 3, r = idx >> 8;
       float o = 0.f;
@@ -283,6 +238,7 @@ __global__ __launch_bounds__(64 * kDecWaves) void gemm2_decode_kernel(Problem pb
     }
     __syncthreads();
   }
+
 }
 
 void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* cbuf, int n_slots, hipStream_t stream) {
@@ -294,8 +250,8 @@ void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* cbuf, int n_s
 void launch_gemm2_decode(const Problem& pb, const Plan& pl, const float* cbuf, float* obuf, int n_slots,
                          hipStream_t stream) {
   if (n_slots <= 0) return;
-  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(pb.H / kDec2Cols, n_slots), dim3(64 * kDecWaves), 0, stream,
-                     pb, pl, cbuf, obuf);
+  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(pb.H / kDec2Cols, n_slots), dim3(64 * kDecWaves), 0, stream, pb, pl,
+                     cbuf, obuf);
 }
 
 }  // namespace moefp8

@@ -466,31 +466,38 @@ __global__ __launch_bounds__(kPfThreads) void gemm2_prefill_kernel(Problem pb, P
   }
 }
 
-// One workgroup per token: fixed ascending-expert sum of its pair rows, bf16 RNE.
+// Workgroup = (token, 1024 columns): fixed ascending-expert sum of the token's pair rows from
+// zero (the index_add_ order of main.py:241), bf16 RNE (main.py:243); zero rows for tokens
+// without a local expert.
+constexpr int kCombineCols = 1024;
+
 __global__ __launch_bounds__(256) void combine_kernel(const int* __restrict__ tok_slot,
                                                       const float* __restrict__ obuf,
                                                       uint16_t* __restrict__ out, int H) {
   const int t = blockIdx.x;
+  const int c = blockIdx.y * kCombineCols + 4 * threadIdx.x;
   int slots[kTopK];
 #pragma unroll
   for (int k = 0; k < kTopK; k++) slots[k] = tok_slot[(size_t)t * kTopK + k];
-  const int H4 = H >> 2;
-  for (int c = threadIdx.x; c < H4; c += blockDim.x) {
-    float4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (c >= H) return;
+  float4 v[kTopK];
 #pragma unroll
-    for (int k = 0; k < kTopK; k++) {
-      if (slots[k] < 0) break;
-      const float4 v = reinterpret_cast<const float4*>(obuf + (size_t)slots[k] * H)[c];
-      acc.x += v.x;
-      acc.y += v.y;
-      acc.z += v.z;
-      acc.w += v.w;
-    }
-    uint2 o;
-    o.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
-    o.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
-    reinterpret_cast<uint2*>(out + (size_t)t * H)[c] = o;
+  for (int k = 0; k < kTopK; k++)
+    v[k] = slots[k] >= 0 ? *reinterpret_cast<const float4*>(obuf + (size_t)slots[k] * H + c)
+                         : float4{0.f, 0.f, 0.f, 0.f};
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < kTopK; k++) {
+    if (slots[k] < 0) break;
+    acc.x += v[k].x;
+    acc.y += v[k].y;
+    acc.z += v[k].z;
+    acc.w += v[k].w;
   }
+  uint2 o;
+  o.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
+  o.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
+  *reinterpret_cast<uint2*>(out + (size_t)t * H + c) = o;
 }
 
 template <int BM>
@@ -533,7 +540,8 @@ void launch_gemm2_prefill(const Problem& pb, const Plan& pl, int tile_m, const C
 
 void launch_combine(const Plan& pl, const float* obuf, uint16_t* out, int T, int H, hipStream_t stream) {
   if (T <= 0) return;
-  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, stream, pl.tok_slot, obuf, out, H);
+  hipLaunchKernelGGL(combine_kernel, dim3(T, (H + kCombineCols - 1) / kCombineCols), dim3(256), 0, stream,
+                     pl.tok_slot, obuf, out, H);
 }
 
 }  // namespace moefp8

@@ -119,6 +119,25 @@ static int check_dtype(int dt) { return (dt >= 0 && dt <= 2) ? MOEFP8_OK : MOEFP
 
 using namespace moefp8;
 
+// Launch-error check and the optional debug copies that end every moefp8_run.
+static int finish(const moefp8_args* a, const Layout& L, const int* topk_ids, const float* topk_w, const Plan& pl,
+                  hipStream_t s) {
+  if (hipGetLastError() != hipSuccess) return MOEFP8_ERR_LAUNCH;
+  const int64_t T = a->num_tokens;
+  struct Copy {
+    void* dst;
+    const void* src;
+    size_t bytes;
+  } copies[] = {{a->topk_ids, topk_ids, (size_t)T * kTopK * 4},
+                {a->topk_weights, topk_w, (size_t)T * kTopK * 4},
+                {a->expert_offsets, pl.expert_offsets, (size_t)(a->num_local_experts + 1) * 4},
+                {a->permuted_tokens, pl.perm_token, (size_t)L.pmax * 4}};
+  for (const Copy& c : copies)
+    if (c.dst && hipMemcpyAsync(c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return MOEFP8_ERR_LAUNCH;
+  return MOEFP8_OK;
+}
+
 extern "C" {
 
 int moefp8_abi_version(void) { return MOEFP8_ABI_VERSION; }
@@ -221,9 +240,31 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   auto mark = [&](int i) {
     if (ev) (void)hipEventRecord(ev[i], s);
   };
-  mark(0);
   MagInputs mag = {a->hidden_states, a->hidden_states_scale, a->gemm1_weights_scale, a->gemm2_weights_scale,
                    H, I, E_local, tok_a2, esig};
+  if (T <= kDecodeMaxT) {
+    // small T: 3 launches -- routing+permutation, GEMM1, GEMM2+combine
+    mark(0);
+    launch_route_permute_small(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, (int)T,
+                               a->routed_scaling_factor, mag, a->local_expert_offset, tile_m, topk_ids, topk_w,
+                               const_cast<int*>(pl.expert_offsets), const_cast<int*>(pl.perm_token),
+                               const_cast<float*>(pl.perm_w), const_cast<int*>(pl.tok_slot),
+                               const_cast<int*>(pl.active), const_cast<int*>(pl.mtile_offsets),
+                               const_cast<int*>(pl.info), const_cast<uint8_t*>(pl.exact), s);
+    mark(1);
+    mark(2);
+    const int n_slots = (int)(L.pmax < E_local ? L.pmax : E_local);
+    float* cbuf = reinterpret_cast<float*>(ws + L.cbuf);
+    float* obuf = reinterpret_cast<float*>(ws + L.obuf);
+    launch_gemm1_decode(pb, pl, cbuf, n_slots, s);
+    mark(3);
+    launch_gemm2_decode(pb, pl, cbuf, obuf, n_slots, s);
+    mark(4);
+    launch_combine(pl, obuf, a->output, (int)T, H, s);
+    mark(5);
+    return finish(a, L, topk_ids, topk_w, pl, s);
+  }
+  mark(0);
   launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,
                topk_ids, topk_w, &mag, s);
   mark(1);
@@ -233,13 +274,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
                  const_cast<int*>(pl.info), tok_a2, esig, I, const_cast<uint8_t*>(pl.exact), s);
   mark(2);
   float* obuf = reinterpret_cast<float*>(ws + L.obuf);
-  if (T <= kDecodeMaxT) {
-    const int n_slots = (int)(L.pmax < E_local ? L.pmax : E_local);
-    float* cbuf = reinterpret_cast<float*>(ws + L.cbuf);
-    launch_gemm1_decode(pb, pl, cbuf, n_slots, s);
-    mark(3);
-    launch_gemm2_decode(pb, pl, cbuf, obuf, n_slots, s);
-  } else {
+  {
     CSplit cs;
     cs.q = ws + L.c_q;
     cs.plane = L.c_plane;
@@ -253,20 +288,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   mark(4);
   launch_combine(pl, obuf, a->output, (int)T, H, s);
   mark(5);
-
-  if (hipGetLastError() != hipSuccess) return MOEFP8_ERR_LAUNCH;
-  struct Copy {
-    void* dst;
-    const void* src;
-    size_t bytes;
-  } copies[] = {{a->topk_ids, topk_ids, (size_t)T * kTopK * 4},
-                {a->topk_weights, topk_w, (size_t)T * kTopK * 4},
-                {a->expert_offsets, pl.expert_offsets, (size_t)(E_local + 1) * 4},
-                {a->permuted_tokens, pl.perm_token, (size_t)L.pmax * 4}};
-  for (const Copy& c : copies)
-    if (c.dst && hipMemcpyAsync(c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice, s) != hipSuccess)
-      return MOEFP8_ERR_LAUNCH;
-  return MOEFP8_OK;
+  return finish(a, L, topk_ids, topk_w, pl, s);
 }
 
 }  // extern "C"

@@ -29,6 +29,12 @@ void launch_permute(const int* topk_ids, const float* topk_w, int T, int E_local
                     int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
                     uint8_t* perm_exact, hipStream_t stream);
 
+// T <= 64: routing, magnitude estimates, flags and permutation in one single-workgroup launch.
+void launch_route_permute_small(const void* logits, int logits_dt, const void* bias, int bias_dt, int T, float rsf,
+                                const MagInputs& mag, int offset, int tile_m, int* topk_ids, float* topk_w,
+                                int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
+                                int* mtile_offsets, int* info, uint8_t* perm_exact, hipStream_t stream);
+
 // Pointers into the caller's workspace produced by routing + permutation.
 struct Plan {
   const int* expert_offsets;  // [E_local + 1]
@@ -53,6 +59,8 @@ struct Problem {
 
 // Small-T path: weight-streaming GEMM1 (+SwiGLU, fp32 C) and GEMM2 (quantise C on load).
 void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* cbuf, int n_slots, hipStream_t stream);
+// GEMM2 for small T: workgroup = (active expert, 64 H columns), 8 waves split K.
+constexpr int kDec2Cols = 64;
 void launch_gemm2_decode(const Problem& pb, const Plan& pl, const float* cbuf, float* obuf, int n_slots,
                          hipStream_t stream);
 
