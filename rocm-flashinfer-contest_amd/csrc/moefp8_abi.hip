@@ -243,15 +243,16 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   MagInputs mag = {a->hidden_states, a->hidden_states_scale, a->gemm1_weights_scale, a->gemm2_weights_scale,
                    H, I, E_local, tok_a2, esig};
   if (T <= kDecodeMaxT) {
-    // small T: 3 launches -- routing+permutation, GEMM1, GEMM2+combine
+    // small T: routing (+ scale estimates), permutation, GEMM1, GEMM2, combine
     mark(0);
-    launch_route_permute_small(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, (int)T,
-                               a->routed_scaling_factor, mag, a->local_expert_offset, tile_m, topk_ids, topk_w,
-                               const_cast<int*>(pl.expert_offsets), const_cast<int*>(pl.perm_token),
-                               const_cast<float*>(pl.perm_w), const_cast<int*>(pl.tok_slot),
-                               const_cast<int*>(pl.active), const_cast<int*>(pl.mtile_offsets),
-                               const_cast<int*>(pl.info), const_cast<uint8_t*>(pl.exact), s);
+    launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,
+                 topk_ids, topk_w, &mag, s);
     mark(1);
+    launch_permute_small(topk_ids, topk_w, (int)T, E_local, a->local_expert_offset, tile_m,
+                         const_cast<int*>(pl.expert_offsets), const_cast<int*>(pl.perm_token),
+                         const_cast<float*>(pl.perm_w), const_cast<int*>(pl.tok_slot), const_cast<int*>(pl.active),
+                         const_cast<int*>(pl.mtile_offsets), const_cast<int*>(pl.info), tok_a2, esig, I,
+                         const_cast<uint8_t*>(pl.exact), s);
     mark(2);
     const int n_slots = (int)(L.pmax < E_local ? L.pmax : E_local);
     float* cbuf = reinterpret_cast<float*>(ws + L.cbuf);

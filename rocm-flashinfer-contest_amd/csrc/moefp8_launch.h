@@ -29,11 +29,11 @@ void launch_permute(const int* topk_ids, const float* topk_w, int T, int E_local
                     int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
                     uint8_t* perm_exact, hipStream_t stream);
 
-// T <= 64: routing, magnitude estimates, flags and permutation in one single-workgroup launch.
-void launch_route_permute_small(const void* logits, int logits_dt, const void* bias, int bias_dt, int T, float rsf,
-                                const MagInputs& mag, int offset, int tile_m, int* topk_ids, float* topk_w,
-                                int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
-                                int* mtile_offsets, int* info, uint8_t* perm_exact, hipStream_t stream);
+// The same permutation for T <= 64 in one workgroup with no serial loop.
+void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset, int tile_m,
+                          int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
+                          int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
+                          uint8_t* perm_exact, hipStream_t stream);
 
 // Pointers into the caller's workspace produced by routing + permutation.
 struct Plan {

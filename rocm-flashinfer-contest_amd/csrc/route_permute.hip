@@ -33,25 +33,47 @@ struct MagArgs {
   float* esig;             // [E, 2]
 };
 
-__device__ float wave_max_batched(const float* p, int n);
+// Scale estimates of local expert e by one workgroup of 256 threads.  W13 has exactly
+// twice as many scale blocks as W2 (2I/128 x H/128 against H/128 x I/128), so one
+// predicated batch of 8 + 4 loads per thread covers both tensors of the full-size
+// expert (1792 + 896 scales) in a single memory round trip.
+constexpr int kSigmaThreads = 256;
 
 __device__ void expert_sigma_block(const MagArgs& mg, int e) {
-  __shared__ float red[2][4];
-  const int n13 = (2 * mg.I / kBlock) * (mg.H / kBlock), n2 = (mg.H / kBlock) * (mg.I / kBlock);
-  const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  // wave w reduces the w-th quarter of each scale tensor
-  const int q13 = (n13 + nw - 1) / nw, q2 = (n2 + nw - 1) / nw;
-  const int b13 = min(n13, wave * q13), b2 = min(n2, wave * q2);
-  const float m13 = wave_max_batched(mg.s13 + (size_t)e * n13 + b13, min(n13, b13 + q13) - b13);
-  const float m2 = wave_max_batched(mg.s2 + (size_t)e * n2 + b2, min(n2, b2 + q2) - b2);
+  __shared__ float red[2][kSigmaThreads / kWave];
+  const int n2 = (mg.H / kBlock) * (mg.I / kBlock), n13 = 2 * n2;
+  const float* p13 = mg.s13 + (size_t)e * n13;
+  const float* p2 = mg.s2 + (size_t)e * n2;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  float m13 = 0.f, m2 = 0.f;
+  for (int i0 = 0; i0 < n2; i0 += 4 * kSigmaThreads) {
+    float v13[8], v2[4];
+#pragma unroll
+    for (int it = 0; it < 8; it++) {
+      const int i = 2 * i0 + it * kSigmaThreads + tid;
+      v13[it] = i < n13 ? p13[i] : 0.f;
+    }
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+      const int i = i0 + it * kSigmaThreads + tid;
+      v2[it] = i < n2 ? p2[i] : 0.f;
+    }
+#pragma unroll
+    for (int it = 0; it < 8; it++) m13 = fmaxf(m13, v13[it]);
+#pragma unroll
+    for (int it = 0; it < 4; it++) m2 = fmaxf(m2, v2[it]);
+  }
+  m13 = wave_max_f32(m13);
+  m2 = wave_max_f32(m2);
   if (lane_id() == 0) {
     red[0][wave] = m13;
     red[1][wave] = m2;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     float a = red[0][0], b = red[1][0];
-    for (int w = 1; w < (int)(blockDim.x >> 6); w++) {
+#pragma unroll
+    for (int w = 1; w < kSigmaThreads / kWave; w++) {
       a = fmaxf(a, red[0][w]);
       b = fmaxf(b, red[1][w]);
     }
@@ -91,37 +113,12 @@ __device__ float token_sq_norm(const uint8_t* hidden, const float* hscale, int H
       a2 += ss * sc[it] * sc[it];
     }
   }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) a2 += shfl_xor_f(a2, off);
-  return a2;
+  return wave_sum_f32(a2);
 }
 
-// Largest of n floats (one wavefront, loads in predicated batches of 16 per lane).
-__device__ float wave_max_batched(const float* p, int n) {
+// The 4 logits of lane l (experts 4l..4l+3) of token t, as fp32.
+__device__ __forceinline__ void load_logits(const void* logits, int logits_dt, int64_t t, float (&x)[4]) {
   const int lane = lane_id();
-  float m = 0.f;
-  for (int i0 = 0; i0 < n; i0 += 16 * kWave) {
-    float v[16];
-#pragma unroll
-    for (int it = 0; it < 16; it++) {
-      const int i = i0 + it * kWave + lane;
-      v[it] = i < n ? p[i] : 0.f;
-    }
-#pragma unroll
-    for (int it = 0; it < 16; it++) m = fmaxf(m, v[it]);
-  }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, shfl_xor_f(m, off));
-  return m;
-}
-
-// Routing of token t by one wavefront (main.py:139-165); lane l owns experts 4l..4l+3, so
-// lanes 8g..8g+7 own group g.  Lanes 0..7 return the j-th selected id (ascending) and its
-// weight in *id / *w; other lanes return -1.
-__device__ void route_token(const void* logits, int logits_dt, const float (&b)[4], int64_t t, float rsf, int* id_out,
-                            float* w_out) {
-  const int lane = lane_id();
-  float x[4];
   if (logits_dt == 0) {
     const float4 v = reinterpret_cast<const float4*>(logits)[t * (kEGlobal / 4) + lane];
     x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
@@ -129,6 +126,22 @@ __device__ void route_token(const void* logits, int logits_dt, const float (&b)[
 #pragma unroll
     for (int i = 0; i < 4; i++) x[i] = load_as_f32(logits, logits_dt, t * kEGlobal + 4 * lane + i);
   }
+}
+
+// Merge of two (largest, second largest) pairs.
+__device__ __forceinline__ void merge_top2(float& m1, float& m2, float o1, float o2) {
+  const float n2 = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
+  m1 = fmaxf(m1, o1);
+  m2 = n2;
+}
+
+// Routing of one token by one wavefront (main.py:139-165); lane l owns experts 4l..4l+3
+// (logits x, bias b), so lanes 8g..8g+7 own group g.  Lanes 0..7 return the j-th selected
+// id (ascending) and its weight in *id / *w; other lanes return -1.  Cross-lane steps use
+// DPP inside rows of 16 lanes and readlane / ballot across rows, so every selected expert
+// is a wave-uniform value and no step waits on an LDS round trip.
+__device__ void route_token(const float (&x)[4], const float (&b)[4], float rsf, int* id_out, float* w_out) {
+  const int lane = lane_id();
   float s[4], sb[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
@@ -136,66 +149,50 @@ __device__ void route_token(const void* logits, int logits_dt, const float (&b)[
     sb[i] = s[i] + b[i];                                  // main.py:148
   }
 
-  // per-group sum of the two largest sb (main.py:151-153): lane top-2, then merge over 8 lanes
+  // per-group sum of the two largest sb (main.py:151-153): lane top-2, then merged with the
+  // partners at distance 1 and 2 and the mirror lane of the 8-lane group
   float m1 = fmaxf(sb[0], sb[1]), m2 = fminf(sb[0], sb[1]);
 #pragma unroll
-  for (int i = 2; i < 4; i++) {
-    const float v = sb[i];
-    const float n2 = fmaxf(fminf(m1, v), m2);
-    m1 = fmaxf(m1, v);
-    m2 = n2;
-  }
-#pragma unroll
-  for (int off = 1; off < 8; off <<= 1) {
-    const float o1 = shfl_xor_f(m1, off), o2 = shfl_xor_f(m2, off);
-    const float n2 = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
-    m1 = fmaxf(m1, o1);
-    m2 = n2;
-  }
+  for (int i = 2; i < 4; i++) merge_top2(m1, m2, sb[i], -INFINITY);
+  merge_top2(m1, m2, dpp_f32<kDppXor1>(m1), dpp_f32<kDppXor1>(m2));
+  merge_top2(m1, m2, dpp_f32<kDppXor2>(m1), dpp_f32<kDppXor2>(m2));
+  merge_top2(m1, m2, dpp_f32<kDppHalfMirror>(m1), dpp_f32<kDppHalfMirror>(m2));
   const float gscore = m1 + m2;
 
-  // top-4 of 8 groups (main.py:154-156)
+  // top-4 of 8 groups (main.py:154-156): rank of this lane's group against all 8
   const int my_group = lane >> 3;
   int beaten_by = 0;
 #pragma unroll
-  for (int g = 0; g < kNGroup; g++) {
-    const float gs = shfl_f(gscore, 8 * g);
-    beaten_by += ranks_before(gs, g, gscore, my_group) ? 1 : 0;
-  }
+  for (int g = 0; g < kNGroup; g++) beaten_by += ranks_before(readlane_f32(gscore, 8 * g), g, gscore, my_group);
   const bool group_kept = beaten_by < kTopKGroup;
 
-  // top-8 experts inside the kept groups (main.py:158-160), one arg-max per round
-  bool alive[4];
+  // top-8 experts inside the kept groups (main.py:158-160): per round the largest key
+  // over the wave; ties go to the lowest lane (= lowest expert id) via the ballot and to
+  // the lowest slot inside the lane via the strict comparison
+  uint32_t key[4];
 #pragma unroll
-  for (int i = 0; i < 4; i++) alive[i] = group_kept;
+  for (int i = 0; i < 4; i++) key[i] = group_kept ? order_key(sb[i]) : 0u;
   int sel[kTopK];
 #pragma unroll
   for (int r = 0; r < kTopK; r++) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    uint32_t lk = key[0];
+    int li = 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      if (alive[i] && ranks_before(sb[i], 4 * lane + i, bv, bi)) {
-        bv = sb[i];
-        bi = 4 * lane + i;
+    for (int i = 1; i < 4; i++)
+      if (key[i] > lk) {
+        lk = key[i];
+        li = i;
       }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = shfl_xor_f(bv, off);
-      const int oi = shfl_xor_i(bi, off);
-      if (ranks_before(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
-    sel[r] = bi;
+    const uint32_t wk = wave_max_u32(lk);
+    const int owner = (int)__builtin_ctzll(__ballot(lk == wk));
+    const int slot = __builtin_amdgcn_readlane(li, owner);
+    sel[r] = 4 * owner + slot;
 #pragma unroll
     for (int i = 0; i < 4; i++)
-      if (bi == 4 * lane + i) alive[i] = false;
+      if (lane == owner && i == slot) key[i] = 0u;
   }
 
-  // ascending id order (odd-even transposition network, 8 elements)
+  // ascending id order (odd-even transposition network on wave-uniform values)
 #pragma unroll
   for (int pass = 0; pass < kTopK; pass++) {
 #pragma unroll
@@ -212,7 +209,7 @@ __device__ void route_token(const void* logits, int logits_dt, const float (&b)[
   for (int j = 0; j < kTopK; j++) {
     const int owner = sel[j] >> 2, slot = sel[j] & 3;
     const float mine = slot == 0 ? s[0] : slot == 1 ? s[1] : slot == 2 ? s[2] : s[3];
-    s_sel[j] = __shfl(mine, owner, kWave);
+    s_sel[j] = readlane_f32(mine, owner);
   }
   float acc = s_sel[0];
 #pragma unroll
@@ -234,31 +231,35 @@ __device__ void route_token(const void* logits, int logits_dt, const float (&b)[
   }
 }
 
-// One wavefront per token.
-__global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ logits, int logits_dt,
-                                                    const void* __restrict__ bias, int bias_dt, int64_t T,
-                                                    float rsf, int* __restrict__ topk_ids,
-                                                    float* __restrict__ topk_w, int token_blocks, MagArgs mg) {
-  if ((int)blockIdx.x >= token_blocks) {                 // trailing blocks: one per local expert
+// One wavefront per token (kSigmaThreads / 64 tokens per block), plus one trailing
+// block per local expert for the weight-scale estimates.
+__global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __restrict__ logits, int logits_dt,
+                                                              const void* __restrict__ bias, int bias_dt, int64_t T,
+                                                              float rsf, int* __restrict__ topk_ids,
+                                                              float* __restrict__ topk_w, int token_blocks,
+                                                              MagArgs mg) {
+  if ((int)blockIdx.x >= token_blocks) {
     expert_sigma_block(mg, blockIdx.x - token_blocks);
     return;
   }
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
-  const int waves_per_block = blockDim.x >> 6;
+  constexpr int kWavesPerBlock = kSigmaThreads / kWave;
   float b[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) b[i] = load_as_f32(bias, bias_dt, 4 * lane + i);
 
-  for (int64_t t = (int64_t)blockIdx.x * waves_per_block + wave; t < T;
-       t += (int64_t)token_blocks * waves_per_block) {
+  for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wave; t < T;
+       t += (int64_t)token_blocks * kWavesPerBlock) {
+    float x[4];
+    load_logits(logits, logits_dt, t, x);       // issued before the hidden-row loads
     if (mg.hidden) {
       const float a2 = token_sq_norm(mg.hidden, mg.hscale, mg.H, T, t);
       if (lane == 0) mg.tok_a2[t] = a2;
     }
     int id;
     float w;
-    route_token(logits, logits_dt, b, t, rsf, &id, &w);
+    route_token(x, b, rsf, &id, &w);
     if (lane < kTopK) {
       topk_ids[t * kTopK + lane] = id;
       topk_w[t * kTopK + lane] = w;
@@ -274,7 +275,6 @@ __global__ __launch_bounds__(256) void route_kernel(const void* __restrict__ log
 //   active[]        local experts with >= 1 token, ascending; info[] totals
 constexpr int kPermThreads = 1024;
 constexpr int kPermWaves = kPermThreads / kWave;
-constexpr int kSmallT = 64;
 
 __global__ __launch_bounds__(kPermThreads) void permute_kernel(
     const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int E_local, int offset,
@@ -377,163 +377,97 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
   }
 }
 
-// Small-T front end (T <= kSmallT): routing, token norms, expert weight-scale estimates,
-// exact-product flags and the stable permutation in ONE workgroup (one launch instead of
-// two).  Wave w routes tokens w, w+16, ...; wave 0 then ranks all (<= 64) tokens with
-// ballots, so pairs come out expert-major and token-ascending as in main.py:218-225.
-__global__ __launch_bounds__(kPermThreads) void route_permute_small_kernel(
-    const void* __restrict__ logits, int logits_dt, const void* __restrict__ bias, int bias_dt, int T, float rsf,
-    MagArgs mg, int offset, int tile_m, int* __restrict__ topk_ids, float* __restrict__ topk_w,
+// Stable permutation for T <= 64 (one workgroup, one thread per (token, k) pair).  A 64-bit
+// LDS mask of the tokens that picked each local expert gives its count (popcount) and each
+// pair's rank inside the expert (popcount of the lower tokens), so pairs come out
+// expert-major and token-ascending as in main.py:218-225 with no serial loop; the offsets
+// are exclusive prefix sums built from one ballot per bit (counts are <= 64).
+constexpr int kSmallT = 64;
+constexpr int kSmallPermThreads = kSmallT * kTopK;
+
+__global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
+    const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int E_local, int offset, int tile_m,
     int* __restrict__ expert_offsets, int* __restrict__ perm_token, float* __restrict__ perm_w,
     int* __restrict__ tok_slot, int* __restrict__ active, int* __restrict__ mtile_offsets, int* __restrict__ info,
-    uint8_t* __restrict__ perm_exact) {
-  __shared__ int ids_s[kSmallT][kTopK];
-  __shared__ float w_s[kSmallT][kTopK];
-  __shared__ float a2_s[kSmallT];
-  __shared__ int cnt[kEGlobal];
-  __shared__ int base[kEGlobal];
-  __shared__ int act_s[kEGlobal];
-  __shared__ int n_act_s;
-  __shared__ float sig_s[kEGlobal][2];
+    const float* __restrict__ tok_a2, const float* __restrict__ esig, float sqrt_i, uint8_t* __restrict__ perm_exact) {
+  __shared__ unsigned long long tmask[kEGlobal];
+  __shared__ int base_s[kEGlobal];
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-  const int E_local = mg.E_local;
+  const int t = tid >> 3, j = tid & 7;
+  const bool in = t < T;
+  int le = -1;
+  float w = 0.f, a2 = 0.f;
+  if (in) {
+    le = topk_ids[tid] - offset;
+    w = topk_w[tid];
+    a2 = tok_a2[t];
+  }
+  const bool local = in && le >= 0 && le < E_local;
+  for (int e = tid; e < E_local; e += kSmallPermThreads) tmask[e] = 0ull;
+  __syncthreads();
+  if (local) atomicOr(&tmask[le], 1ull << t);
+  __syncthreads();
 
-  // weight-scale estimates of every local expert (independent of the routing, so their loads
-  // overlap it): wave w takes experts w, w+16, ...
-  const int n13 = (2 * mg.I / kBlock) * (mg.H / kBlock), n2 = (mg.H / kBlock) * (mg.I / kBlock);
-  for (int e = wave; e < E_local; e += kPermWaves) {
-    const float m13 = wave_max_batched(mg.s13 + (size_t)e * n13, n13);
-    const float m2 = wave_max_batched(mg.s2 + (size_t)e * n2, n2);
-    if (lane == 0) {
-      sig_s[e][0] = m13 * (448.0f / 3.0f);
-      sig_s[e][1] = m2 * (448.0f / 3.0f);
-    }
-  }
-  float b[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) b[i] = load_as_f32(bias, bias_dt, 4 * lane + i);
-  for (int t = wave; t < T; t += kPermWaves) {
-    const float a2 = token_sq_norm(mg.hidden, mg.hscale, mg.H, T, t);
-    int id;
-    float w;
-    route_token(logits, logits_dt, b, t, rsf, &id, &w);
-    if (lane < kTopK) {
-      ids_s[t][lane] = id;
-      w_s[t][lane] = w;
-      topk_ids[t * kTopK + lane] = id;
-      topk_w[t * kTopK + lane] = w;
-    }
-    if (lane == 0) a2_s[t] = a2;
-  }
-  for (int e = tid; e < E_local; e += kPermThreads) cnt[e] = 0;
-  __syncthreads();
-  if (tid < T * kTopK) {
-    const int le = ids_s[tid >> 3][tid & 7] - offset;
-    if (le >= 0 && le < E_local) atomicAdd(&cnt[le], 1);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0, n_act = 0, mt = 0;
-    for (int e = 0; e < E_local; e++) {
-      expert_offsets[e] = run;
-      mtile_offsets[e] = mt;
-      base[e] = run;
-      run += cnt[e];
-      mt += (cnt[e] + tile_m - 1) / tile_m;
-      if (cnt[e] > 0) {
-        active[n_act] = e;
-        act_s[n_act++] = e;
-      }
-    }
-    expert_offsets[E_local] = run;
-    mtile_offsets[E_local] = mt;
-    info[0] = run;
-    info[1] = n_act;
-    info[2] = mt;
-    n_act_s = n_act;
-  }
-  __syncthreads();
   if (wave == 0) {
-    const int t = lane;
-    int les[kTopK], slots[kTopK];
-    int n = 0;
+    int carry_p = 0, carry_mt = 0, carry_a = 0;
+    for (int e0 = 0; e0 < E_local; e0 += kWave) {
+      const int e = e0 + lane;
+      const int c = e < E_local ? __popcll(tmask[e]) : 0;
+      const int mt = (c + tile_m - 1) / tile_m;
+      int pc = 0, pm = 0;
 #pragma unroll
-    for (int k = 0; k < kTopK; k++) {
-      les[k] = -1;
-      slots[k] = 0;
-    }
-    if (t < T) {
-#pragma unroll
-      for (int j = 0; j < kTopK; j++) {
-        const int le = ids_s[t][j] - offset;
-        if (le >= 0 && le < E_local) {
-#pragma unroll
-          for (int k = 0; k < kTopK; k++)
-            if (k == n) {
-              les[k] = le;
-              slots[k] = j;
-            }
-          n++;
-        }
+      for (int bit = 0; bit < 7; bit++) {
+        pc += lanes_below(__ballot((c >> bit) & 1)) << bit;
+        pm += lanes_below(__ballot((mt >> bit) & 1)) << bit;
       }
-    }
-    int ptr = 0;
-    int pos_k[kTopK];
-#pragma unroll
-    for (int k = 0; k < kTopK; k++) pos_k[k] = -1;
-    const float sqrt_i = sqrtf((float)mg.I);
-    for (int a = 0; a < n_act_s; a++) {
-      const int e = act_s[a];
-      int cur = -1;
-#pragma unroll
-      for (int k = 0; k < kTopK; k++)
-        if (k == ptr) cur = les[k];
-      const bool pick = ptr < n && cur == e;
-      const uint64_t m = __ballot(pick);
-      if (pick) {
-        const int pos = base[e] + __popcll(m & ((1ull << lane) - 1ull));
-        int slot = 0;
-#pragma unroll
-        for (int k = 0; k < kTopK; k++)
-          if (k == ptr) {
-            slot = slots[k];
-            pos_k[k] = pos;
-          }
-        const float w = w_s[t][slot];
-        perm_token[pos] = t;
-        perm_w[pos] = w;
-        perm_exact[pos] = needs_exact_products(a2_s[t], w, sig_s[e][0], sig_s[e][1], sqrt_i);
-        ptr++;
+      const uint64_t act = __ballot(c > 0);
+      if (e < E_local) {
+        expert_offsets[e] = carry_p + pc;
+        mtile_offsets[e] = carry_mt + pm;
+        base_s[e] = carry_p + pc;
+        if (c > 0) active[carry_a + lanes_below(act)] = e;
       }
+      carry_p += __builtin_amdgcn_readlane(pc + c, kWave - 1);
+      carry_mt += __builtin_amdgcn_readlane(pm + mt, kWave - 1);
+      carry_a += (int)__popcll(act);
     }
-    if (t < T) {
-#pragma unroll
-      for (int k = 0; k < kTopK; k++) tok_slot[t * kTopK + k] = pos_k[k];
+    if (lane == 0) {
+      expert_offsets[E_local] = carry_p;
+      mtile_offsets[E_local] = carry_mt;
+      info[0] = carry_p;    // P
+      info[1] = carry_a;    // active experts
+      info[2] = carry_mt;   // m-tiles of height tile_m
     }
   }
+  __syncthreads();
+
+  // k = rank of this pair among its token's local pairs (a wave holds 8 whole tokens)
+  const uint32_t tb = (uint32_t)(__ballot(local) >> (8 * (lane >> 3))) & 0xffu;
+  const int n = __popc(tb);
+  if (local) {
+    const int k = __popc(tb & ((1u << j) - 1u));
+    const int pos = base_s[le] + (int)__popcll(tmask[le] & ((1ull << t) - 1ull));
+    perm_token[pos] = t;
+    perm_w[pos] = w;
+    perm_exact[pos] = needs_exact_products(a2, w, esig[2 * le], esig[2 * le + 1], sqrt_i);
+    tok_slot[t * kTopK + k] = pos;
+  }
+  if (in && j >= n) tok_slot[t * kTopK + j] = -1;
 }
 
-void launch_route_permute_small(const void* logits, int logits_dt, const void* bias, int bias_dt, int T, float rsf,
-                                const MagInputs& mag, int offset, int tile_m, int* topk_ids, float* topk_w,
-                                int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
-                                int* mtile_offsets, int* info, uint8_t* perm_exact, hipStream_t stream) {
-  MagArgs mg = {};
-  mg.hidden = mag.hidden;
-  mg.hscale = mag.hscale;
-  mg.s13 = mag.s13;
-  mg.s2 = mag.s2;
-  mg.H = mag.H;
-  mg.I = mag.I;
-  mg.E_local = mag.E_local;
-  hipLaunchKernelGGL(route_permute_small_kernel, dim3(1), dim3(kPermThreads), 0, stream, logits, logits_dt, bias,
-                     bias_dt, T, rsf, mg, offset, tile_m, topk_ids, topk_w, expert_offsets, perm_token, perm_w,
-                     tok_slot, active, mtile_offsets, info, perm_exact);
+void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset, int tile_m,
+                          int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
+                          int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
+                          uint8_t* perm_exact, hipStream_t stream) {
+  hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(kSmallPermThreads), 0, stream, topk_ids, topk_w, T,
+                     E_local, offset, tile_m, expert_offsets, perm_token, perm_w, tok_slot, active, mtile_offsets,
+                     info, tok_a2, esig, sqrtf((float)I), perm_exact);
 }
 
 void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
                   int* topk_ids, float* topk_w, const MagInputs* mag, hipStream_t stream) {
   if (T <= 0) return;
-  const int64_t tokens_per_block = 4;
+  const int64_t tokens_per_block = kSigmaThreads / kWave;
   int64_t blocks = (T + tokens_per_block - 1) / tokens_per_block;
   if (blocks > 4096) blocks = 4096;
   MagArgs mg = {};
@@ -550,7 +484,7 @@ void launch_route(const void* logits, int logits_dt, const void* bias, int bias_
     mg.esig = mag->esig;
     extra = mag->E_local;
   }
-  hipLaunchKernelGGL(route_kernel, dim3((unsigned)(blocks + extra)), dim3(256), 0, stream, logits, logits_dt,
+  hipLaunchKernelGGL(route_kernel, dim3((unsigned)(blocks + extra)), dim3(kSigmaThreads), 0, stream, logits, logits_dt,
                      bias, bias_dt, T, rsf, topk_ids, topk_w, (int)blocks, mg);
 }
 
