@@ -1,22 +1,37 @@
-// Small-T expert GEMMs: weight streaming on fp8 MFMA (v_mfma_f32_16x16x128_f8f6f4).
+// Small-T expert GEMMs (T <= 64): balanced weight streams on MFMA.
 //
-// With a few tokens per expert the work is reading each active expert's weights
-// once (HBM bound).  Every workgroup owns one (active expert, column slice) and
-// its waves split K, so even one active expert spreads over hundreds of
-// wavefronts.  Weights and activations go straight from global memory into the
-// MFMA operand registers; the only LDS use is the fixed-order cross-wave sum.
+// With a few tokens per expert the work is reading each active expert's weights once
+// (HBM bound), so both GEMMs are built around one balanced, fully resident round of
+// weight streams.  A workgroup unit is (m-tile, K-slice, 4 consecutive 16-column groups);
+// each of its 4 wavefronts streams the 16 weight rows of its column group through a
+// register ring (several K-blocks of loads in flight) and keeps its 16 x 16 accumulator
+// in registers.  The activation tile of the m-tile is the same for the 4 wavefronts, so
+// it is loaded once per workgroup: each K step a few carrier wavefronts fetch one piece
+// of the activation block and its 16 row scales and publish them through LDS.
+// Per-wavefront activation loads from global memory cost the weight stream about a
+// third of its bandwidth on this chip (measured); sharing them through LDS removes it.
 //
-// GEMM1  G1 = A_e W13_e^T, C = silu(G1[:, I:]) * G1[:, :I]   (main.py:229-233), C in fp32.
-// GEMM2  O = C W2_e^T times the pair's routing weight, summed per token in ascending
-//        expert order and written as bf16 (main.py:234-243); see gemm2_decode_kernel.
+// A persistent grid sized to the resident capacity walks the units.  The K-split S of
+// each GEMM (chosen by the permutation kernel from the m-tile count) is the largest that
+// still fits the grid, so a handful of active experts still spreads over every CU; the S
+// partial sums go to separate rows and the next stage adds them in ascending order.
+//
+// GEMM1       G1 partials = A_e W13_e^T over a K-slice                  (main.py:229-231)
+// activation  C = silu(sum_s G1[:, I:]) * sum_s G1[:, :I]              (main.py:232-233),
+//             stored as f16 hi + lo with one fp32 scale per (pair, 128 columns)
+// GEMM2       O partials = routing weight * C W2_e^T over a K-slice   (main.py:234-241),
+//             exact products of C's f16 hi term (2^-11 relative) and W2 widened to f16
+// The combine kernel then sums each token's pair rows and splits (main.py:242-243).
+// M-tiles flagged for exact products (GEMM1) or for both f16 terms of C (GEMM2) take a
+// simpler per-wavefront path.
 #include "moefp8_device.h"
 #include "moefp8_launch.h"
 
 namespace moefp8 {
 
-constexpr int kDecWaves = 8;             // waves per workgroup (split K)
-constexpr int kDec1Cols = 32;            // C columns per GEMM1 workgroup (32 up + 32 gate rows of W13)
-constexpr int kDec1Unroll = 2;           // GEMM1 K blocks in flight per wave
+constexpr int kDecBlockWaves = 4;            // wavefronts per workgroup = column groups per unit
+constexpr int kDecBlocksPerCU = 5;           // resident workgroups per CU (<= 96 VGPRs)
+constexpr int kDecDepth = 3;                 // K-blocks in flight per wavefront (register ring)
 
 __device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
   const v4i* q = reinterpret_cast<const v4i*>(p);
@@ -24,234 +39,304 @@ __device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
   return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-__global__ __launch_bounds__(64 * kDecWaves) void gemm1_decode_kernel(Problem pb, Plan pl,
-                                                                      float* __restrict__ cbuf) {
-  const int slot = blockIdx.y;
-  if (slot >= pl.info[1]) return;
-  const int e = pl.active[slot];
-  const int row0 = pl.expert_offsets[e];
-  const int M = pl.expert_offsets[e + 1] - row0;
-  const int H = pb.H, I = pb.I, T = pb.T;
-  const int KB = H / kBlock;
-  const int c0 = blockIdx.x * kDec1Cols;
-  const int lane = lane_id(), wave = threadIdx.x >> 6;
-  const int lr = lane & 15, kg = lane >> 4;
-
-  // B rows: subtiles 0,1 = up rows c0+16j+lr, subtiles 2,3 = gate rows I+c0+16(j-2)+lr
-  const uint8_t* wexp = pb.w13 + (size_t)e * 2 * I * H;
-  const uint8_t* brow[4];
+__device__ __forceinline__ void load_v8h4(const _Float16* p, v8h (&y)[4]) {
+  const v8h* q = reinterpret_cast<const v8h*>(p);
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int n = (j < 2 ? c0 + 16 * j : I + c0 + 16 * (j - 2)) + lr;
-    brow[j] = wexp + (size_t)n * H + kg * 32;
-  }
-  const float* s_up = pb.s13 + ((size_t)e * (2 * I / kBlock) + c0 / kBlock) * KB;
-  const float* s_gate = pb.s13 + ((size_t)e * (2 * I / kBlock) + (I + c0) / kBlock) * KB;
+  for (int i = 0; i < 4; i++) y[i] = q[i];
+}
 
-  __shared__ float red[kDecWaves][4][4][64];
+// Unit u -> (m-tile g, K-split s, column block cb of 4 groups), column block fastest.
+struct DecUnit {
+  int g, s, cb;
+};
+__device__ __forceinline__ DecUnit decode_unit(int u, int S, int NCB) {
+  const int rest = u / NCB;
+  return DecUnit{rest / S, rest % S, u - rest * NCB};
+}
 
-  for (int m0 = 0; m0 < M; m0 += 16) {
-    const int ar = m0 + lr;
-    const bool a_ok = ar < M;
-    const uint8_t* arow = pb.hidden + (size_t)pl.perm_token[row0 + (a_ok ? ar : 0)] * H + kg * 32;
-    int tok_d[4];
+// LDS stage of GEMM1: 16 activation rows x 128 e4m3 bytes stored [16-byte chunk][row]
+// (the MFMA operand read, 2 x 16 bytes per lane, is then conflict-free) and the 16 row
+// scales.
+struct alignas(16) G1Stage {
+  uint8_t a[8 * 16 * 16];
+  float sa[16];
+};
+
+// LDS stage of GEMM2: 16 rows of C's f16 hi term x 128 columns, same chunk-major order.
+struct alignas(16) G2Stage {
+  _Float16 a[16 * 16 * 8];
+  float sa[16];
+};
+
+// Steady state of both GEMMs, K step j: the carrier wavefronts write the activation piece
+// of step j (loaded kDecDepth steps earlier) into LDS stage j & 1, the workgroup
+// barrier publishes it, every wavefront computes step j from LDS and its own weight
+// registers, then loads its pieces of step j + kDecDepth.  A stage is rewritten two
+// steps after it was read, i.e. after the barrier that follows every wavefront's read.
+
+__global__ __launch_bounds__(64 * kDecBlockWaves, kDecBlocksPerCU) void gemm1_decode_kernel(Problem pb, Plan pl,
+                                                                                             float* __restrict__ gbuf) {
+  __shared__ G1Stage ring[2];
+  const int n_mt = pl.info[2], S = pl.info[3];
+  const int H = pb.H, I2 = 2 * pb.I, T = pb.T;
+  const int KB = H / kBlock, NCB = I2 / (16 * kDecBlockWaves);
+  const int n_units = n_mt * S * NCB;
+  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+
+  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const DecUnit du = decode_unit(u, S, NCB);
+    const int4 mt = pl.mtiles[du.g];
+    const int e = uniform(mt.x), row0 = uniform(mt.y), M = uniform(mt.z), flags = uniform(mt.w);
+    const int kb0 = du.s * KB / S, n = (du.s + 1) * KB / S - kb0;
+    const int cg = du.cb * kDecBlockWaves + wave;
+    // W13 row cg*16 + lr (columns [0, I) are "up", [I, 2I) "gate"); lane reads k-group kg
+    const uint8_t* bp = pb.w13 + ((size_t)e * I2 + cg * 16 + lr) * H + (size_t)kb0 * kBlock + kg * 32;
+    const float* swp = pb.s13 + ((size_t)e * (I2 / kBlock) + (cg * 16) / kBlock) * KB + kb0;
+    // rows >= M repeat the m-tile's first pair (real data, results discarded)
+    const int tok = pl.perm_token[row0 + (lr < M ? lr : 0)];
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+
+    if (!(flags & kFlagExactProducts)) {
+      // carriers: waves 0/1 publish 16-byte chunk 4q + kg of row lr, wave 0's lanes < 16 the
+      // scale of row lane.  Every wavefront issues the same loads kDecDepth steps ahead
+      // (waves 2/3 repeat waves 0/1's, cache hits): loads under a branch would make the
+      // compiler's wait counting fall back to draining all of them.
+      const uint8_t* asrc = pb.hidden + (size_t)tok * H + (size_t)kb0 * kBlock + (4 * (wave & 1) + kg) * 16;
+      const float* ssrc = pb.hscale + (size_t)kb0 * T + tok;
+      v8i B[kDecDepth];
+      v4i AR[kDecDepth];
+      float SR[kDecDepth], SW[kDecDepth];
+      auto load = [&](int d, int j) {
+        const int jj = min(j, n - 1);
+        B[d] = load_v8i(bp + (size_t)jj * kBlock);
+        AR[d] = *reinterpret_cast<const v4i*>(asrc + (size_t)jj * kBlock);
+        SR[d] = ssrc[(size_t)jj * T];
+        SW[d] = swp[jj];
+      };
+      auto step = [&](int d, int j) {
+        G1Stage& st = ring[j & 1];
+        if (wave < 2) *reinterpret_cast<v4i*>(st.a + wave * 1024 + lane * 16) = AR[d];
+        if (wave == 0 && lane < 16) st.sa[lane] = SR[d];
+        __syncthreads();
+        const v4i x = *reinterpret_cast<const v4i*>(st.a + ((2 * kg) * 16 + lr) * 16);
+        const v4i y = *reinterpret_cast<const v4i*>(st.a + ((2 * kg + 1) * 16 + lr) * 16);
+        const float4 sa = *reinterpret_cast<const float4*>(st.sa + 4 * kg);
+        const float sw = SW[d];
+        const v4f p = mfma16x16x128(__builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7), B[d],
+                                    v4f{0.f, 0.f, 0.f, 0.f});
+        acc[0] += p[0] * (sa.x * sw);
+        acc[1] += p[1] * (sa.y * sw);
+        acc[2] += p[2] * (sa.z * sw);
+        acc[3] += p[3] * (sa.w * sw);
+      };
+#pragma unroll
+      for (int d = 0; d < kDecDepth; d++) load(d, d);
+      // full groups of kDecDepth steps (no early exit, so every prefetch stays where it is
+      // written), then the remaining < kDecDepth steps from the ring without new loads
+      int j = 0;
+      for (; j + kDecDepth <= n; j += kDecDepth) {
+#pragma unroll
+        for (int d = 0; d < kDecDepth; d++) {
+          step(d, j + d);
+          load(d, j + d + kDecDepth);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < kDecDepth - 1; d++)
+        if (j + d < n) step(d, j + d);
+      // the next unit writes stage 0 only after every wavefront has read this unit's last stage
+      __syncthreads();
+    } else {
+      int tok_d[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int dr = 4 * kg + r;
+        tok_d[r] = pl.perm_token[row0 + (dr < M ? dr : 0)];
+      }
+      const uint8_t* ap = pb.hidden + (size_t)tok * H + (size_t)kb0 * kBlock + kg * 32;
+      for (int j = 0; j < n; j++) {
+        const v8i b = load_v8i(bp + (size_t)j * kBlock);
+        const v8i a = load_v8i(ap + (size_t)j * kBlock);
+        float sa[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) sa[r] = pb.hscale[(size_t)(kb0 + j) * T + tok_d[r]];
+        const float sw = swp[j];
+        v8h a16[4], b16[4];
+        widen_fp8_operand(a, a16);
+        widen_fp8_operand(b, b16);
+        const v4f p = mfma_f16_block(a16, b16, v4f{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[r] += p[r] * (sa[r] * sw);
+      }
+    }
+    // D layout: lane holds rows 4*kg + r of column lr
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const int dr = m0 + kg * 4 + r;
-      tok_d[r] = pl.perm_token[row0 + (dr < M ? dr : 0)];
+      const int row = 4 * kg + r;
+      if (row < M) gbuf[((size_t)(row0 + row) * S + du.s) * I2 + cg * 16 + lr] = acc[r];
     }
-    // exact-product sub-tile if any of its 16 pairs is flagged
-    const bool exact = __ballot(lane < 16 && a_ok && pl.exact[row0 + ar]) != 0;
-    v4f acc[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    for (int kb0 = wave; kb0 < KB; kb0 += kDecWaves * kDec1Unroll) {
-      v8i a[kDec1Unroll], b[kDec1Unroll][4];
-      float sa[kDec1Unroll][4], su[kDec1Unroll], sg[kDec1Unroll];
-#pragma unroll
-      for (int u = 0; u < kDec1Unroll; u++) {
-        const int kb = kb0 + u * kDecWaves;
-        if (kb < KB) {
-          a[u] = a_ok ? load_v8i(arow + kb * kBlock) : v8i{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-          for (int j = 0; j < 4; j++) b[u][j] = load_v8i(brow[j] + kb * kBlock);
-#pragma unroll
-          for (int r = 0; r < 4; r++) sa[u][r] = pb.hscale[(size_t)kb * T + tok_d[r]];
-          su[u] = s_up[kb];
-          sg[u] = s_gate[kb];
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kDec1Unroll; u++) {
-        const int kb = kb0 + u * kDecWaves;
-        if (kb < KB) {
-          v8h a16[4];
-          if (exact) widen_fp8_operand(a[u], a16);
-#pragma unroll
-          for (int j = 0; j < 4; j++) {
-            v4f p;
-            if (exact) {
-              v8h b16[4];
-              widen_fp8_operand(b[u][j], b16);
-              p = mfma_f16_block(a16, b16, v4f{0.f, 0.f, 0.f, 0.f});
-            } else {
-              p = mfma16x16x128(a[u], b[u][j], v4f{0.f, 0.f, 0.f, 0.f});
-            }
-            const float sw = j < 2 ? su[u] : sg[u];
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[j][r] += p[r] * (sa[u][r] * sw);
-          }
-        }
-      }
-    }
-
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) red[wave][j][r][lane] = acc[j][r];
-    __syncthreads();
-    // 16 rows x 32 C columns; thread -> (lane', half q, r)
-    for (int idx = threadIdx.x; idx < 16 * kDec1Cols; idx += 64 * kDecWaves) {
-      const int ln = idx & 63, q = (idx >> 6) & 1, r = idx >> 7;
-      float up = 0.f, gate = 0.f;
-#pragma unroll
-      for (int w = 0; w < kDecWaves; w++) {
-        up += red[w][q][r][ln];
-        gate += red[w][q + 2][r][ln];
-      }
-      const int row = m0 + (ln >> 4) * 4 + r;
-      if (row < M) cbuf[(size_t)(row0 + row) * I + c0 + q * 16 + (ln & 15)] = silu_f32(gate) * up;
-    }
-    __syncthreads();
   }
 }
 
-// GEMM2 for small T (main.py:234-241).  Workgroup = (active expert, 64 H
-// columns); its 8 waves split K and a fixed-order LDS sum gives O for each of the expert's
-// pairs, stored routing-weighted in fp32.  C (fp32 from GEMM1) is split on load into two f16
-// terms per 128-block with one fp32 scale and multiplied with W2 widened to f16: exact
-// products, ~2^-22 relative error on C.  The combine kernel then sums each token's pair rows.
-__global__ __launch_bounds__(64 * kDecWaves) void gemm2_decode_kernel(Problem pb, Plan pl,
-                                                                              const float* __restrict__ cbuf,
-                                                                              float* __restrict__ obuf) {
-  const int slot = blockIdx.y;
-  const int n_act = pl.info[1];
-  const int H = pb.H, I = pb.I, T = pb.T;
-  const int h0 = blockIdx.x * kDec2Cols;
-  if (slot >= n_act) return;
-  const int e = pl.active[slot];
-  const int row0 = pl.expert_offsets[e];
-  const int M = pl.expert_offsets[e + 1] - row0;
-  const int KB = I / kBlock;
-  const int HB = H / kBlock;
-  const int lane = lane_id(), wave = threadIdx.x >> 6;
-  const int lr = lane & 15, kg = lane >> 4;
+// One wavefront per (pair p, 128-column block): sums the GEMM1 partials in split order,
+// applies SwiGLU and writes C as two f16 terms with one scale (max |C| -> 448).
+__global__ __launch_bounds__(256) void activation_decode_kernel(int I, Plan pl, const float* __restrict__ gbuf,
+                                                                CHalf ch) {
+  const int P = pl.info[0], S = pl.info[3];
+  const int CB = I / kBlock, I2 = 2 * I;
+  const int w = blockIdx.x * 4 + wave_index();
+  if (w >= P * CB) return;
+  const int p = w / CB, cb = w - p * CB;
+  const int lane = lane_id();
+  const int c = cb * kBlock + 2 * lane;
+  float2 up = {0.f, 0.f}, gate = {0.f, 0.f};
+  for (int s = 0; s < S; s++) {
+    const float* row = gbuf + ((size_t)p * S + s) * I2;
+    const float2 u = *reinterpret_cast<const float2*>(row + c);
+    const float2 g = *reinterpret_cast<const float2*>(row + I + c);
+    up.x += u.x;
+    up.y += u.y;
+    gate.x += g.x;
+    gate.y += g.y;
+  }
+  const float c0 = silu_f32(gate.x) * up.x, c1 = silu_f32(gate.y) * up.y;
+  const float amax = wave_max_f32(fmaxf(fabsf(c0), fabsf(c1)));
+  float inv, scale;
+  split_scale(amax, inv, scale);
+  _Float16 h0, l0, h1, l1;
+  split_f16(c0, inv, h0, l0);
+  split_f16(c1, inv, h1, l1);
+  *reinterpret_cast<v2h*>(ch.hi + (size_t)p * I + c) = v2h{h0, h1};
+  *reinterpret_cast<v2h*>(ch.lo + (size_t)p * I + c) = v2h{l0, l1};
+  if (lane == 0) ch.scale[(size_t)p * CB + cb] = scale;
+}
 
-  const uint8_t* wexp = pb.w2 + (size_t)e * H * I;
-  const uint8_t* brow[4];
-#pragma unroll
-  for (int j = 0; j < 4; j++) brow[j] = wexp + (size_t)(h0 + 16 * j + lr) * I + kg * 32;
-  const float* s_row = pb.s2 + ((size_t)e * HB + h0 / kBlock) * KB;
+__global__ __launch_bounds__(64 * kDecBlockWaves, kDecBlocksPerCU) void gemm2_decode_kernel(Problem pb, Plan pl,
+                                                                                             CHalf ch,
+                                                                                             float* __restrict__ obuf) {
+  __shared__ G2Stage ring[2];
+  const int n_mt = pl.info[2], S = pl.info[4];
+  const int H = pb.H, I = pb.I;
+  const int KB = I / kBlock, HB = H / kBlock, NCB = H / (16 * kDecBlockWaves);
+  const int n_units = n_mt * S * NCB;
+  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
 
-  __shared__ float red[kDecWaves][4][4][64];
+  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const DecUnit du = decode_unit(u, S, NCB);
+    const int4 mt = pl.mtiles[du.g];
+    const int e = uniform(mt.x), row0 = uniform(mt.y), M = uniform(mt.z), flags = uniform(mt.w);
+    const int kb0 = du.s * KB / S, n = (du.s + 1) * KB / S - kb0;
+    const int cg = du.cb * kDecBlockWaves + wave;
+    const uint8_t* bp = pb.w2 + ((size_t)e * H + cg * 16 + lr) * I + (size_t)kb0 * kBlock + kg * 32;
+    const float* swp = pb.s2 + ((size_t)e * HB + (cg * 16) / kBlock) * KB + kb0;
+    const int prow = row0 + (lr < M ? lr : 0);
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
 
-  for (int m0 = 0; m0 < M; m0 += 16) {
-    const int ar = m0 + lr;
-    const bool a_ok = ar < M;
-    const float* crow = cbuf + (size_t)(row0 + (a_ok ? ar : 0)) * I + kg * 32;
-    v4f acc[4];
+    if (!(flags & kFlagTwoTermC)) {
+      // carriers: wave q publishes 16-byte chunk 4q + kg of row lr of C's hi term, wave 0's
+      // lanes < 16 the scale of row lane (all lanes load it: no loads under a branch)
+      const _Float16* asrc = ch.hi + (size_t)prow * I + (size_t)kb0 * kBlock + (4 * wave + kg) * 8;
+      const float* ssrc = ch.scale + (size_t)prow * KB + kb0;
+      v8i B[kDecDepth];
+      v4i AR[kDecDepth];
+      float SR[kDecDepth], SW[kDecDepth];
+      auto load = [&](int d, int j) {
+        const int jj = min(j, n - 1);
+        B[d] = load_v8i(bp + (size_t)jj * kBlock);
+        AR[d] = *reinterpret_cast<const v4i*>(asrc + (size_t)jj * kBlock);
+        SR[d] = ssrc[jj];
+        SW[d] = swp[jj];
+      };
+      auto step = [&](int d, int j) {
+        G2Stage& st = ring[j & 1];
+        *reinterpret_cast<v4i*>(st.a + wave * 512 + lane * 8) = AR[d];
+        if (wave == 0 && lane < 16) st.sa[lane] = SR[d];
+        __syncthreads();
+        v8h ah[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    for (int kb0 = wave; kb0 < KB; kb0 += 2 * kDecWaves) {
-      v8i b[2][4];
-      float cv[2][32];
-      float sw[2];
+        for (int t = 0; t < 4; t++) ah[t] = *reinterpret_cast<const v8h*>(st.a + ((4 * kg + t) * 16 + lr) * 8);
+        const float4 sa = *reinterpret_cast<const float4*>(st.sa + 4 * kg);
+        const float sw = SW[d];
+        v8h b16[4];
+        widen_fp8_operand(B[d], b16);
+        const v4f p = mfma_f16_block(ah, b16, v4f{0.f, 0.f, 0.f, 0.f});
+        acc[0] += p[0] * (sa.x * sw);
+        acc[1] += p[1] * (sa.y * sw);
+        acc[2] += p[2] * (sa.z * sw);
+        acc[3] += p[3] * (sa.w * sw);
+      };
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
-        const int kb = kb0 + u * kDecWaves;
-        if (kb < KB) {
+      for (int d = 0; d < kDecDepth; d++) load(d, d);
+      int j = 0;
+      for (; j + kDecDepth <= n; j += kDecDepth) {
 #pragma unroll
-          for (int j = 0; j < 4; j++) b[u][j] = load_v8i(brow[j] + kb * kBlock);
-          const float4* cp = reinterpret_cast<const float4*>(crow + kb * kBlock);
-#pragma unroll
-          for (int c4 = 0; c4 < 8; c4++) {
-            const float4 v = a_ok ? cp[c4] : float4{0.f, 0.f, 0.f, 0.f};
-            cv[u][4 * c4 + 0] = v.x;
-            cv[u][4 * c4 + 1] = v.y;
-            cv[u][4 * c4 + 2] = v.z;
-            cv[u][4 * c4 + 3] = v.w;
-          }
-          sw[u] = s_row[kb];
+        for (int d = 0; d < kDecDepth; d++) {
+          step(d, j + d);
+          load(d, j + d + kDecDepth);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
-        const int kb = kb0 + u * kDecWaves;
-        if (kb < KB) {
-          float amax = 0.f;
+      for (int d = 0; d < kDecDepth - 1; d++)
+        if (j + d < n) step(d, j + d);
+      __syncthreads();
+    } else {
+      const _Float16* hp = ch.hi + (size_t)prow * I + (size_t)kb0 * kBlock + kg * 32;
+      const _Float16* lp = ch.lo + (size_t)prow * I + (size_t)kb0 * kBlock + kg * 32;
+      const float* sp[4];
 #pragma unroll
-          for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(cv[u][i]));
-          amax = fmaxf(amax, shfl_xor_f(amax, 16));
-          amax = fmaxf(amax, shfl_xor_f(amax, 32));
-          float inv, scale;
-          split_scale(amax, inv, scale);
-          float sa[4];
+      for (int r = 0; r < 4; r++) {
+        const int dr = 4 * kg + r;
+        sp[r] = ch.scale + (size_t)(row0 + (dr < M ? dr : 0)) * KB + kb0;
+      }
+      for (int j = 0; j < n; j++) {
+        const v8i b = load_v8i(bp + (size_t)j * kBlock);
+        v8h ah[4], al[4];
+        load_v8h4(hp + (size_t)j * kBlock, ah);
+        load_v8h4(lp + (size_t)j * kBlock, al);
+        float sa[4];
 #pragma unroll
-          for (int r = 0; r < 4; r++) sa[r] = shfl_f(scale, kg * 4 + r);
-          v8h ch[4], cl[4];
+        for (int r = 0; r < 4; r++) sa[r] = sp[r][j];
+        const float sw = swp[j];
+        v8h b16[4];
+        widen_fp8_operand(b, b16);
+        v4f p = mfma_f16_block(ah, b16, v4f{0.f, 0.f, 0.f, 0.f});
+        p = mfma_f16_block(al, b16, p);
 #pragma unroll
-          for (int i = 0; i < 32; i++) {
-            _Float16 hv, lv;
-            split_f16(cv[u][i], inv, hv, lv);
-            ch[i >> 3][i & 7] = hv;
-            cl[i >> 3][i & 7] = lv;
-          }
-#pragma unroll
-          for (int j = 0; j < 4; j++) {
-            v8h b16[4];
-            widen_fp8_operand(b[u][j], b16);
-            v4f p = mfma_f16_block(ch, b16, v4f{0.f, 0.f, 0.f, 0.f});
-            p = mfma_f16_block(cl, b16, p);
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[j][r] += p[r] * (sa[r] * sw[u]);
-          }
-        }
+        for (int r = 0; r < 4; r++) acc[r] += p[r] * (sa[r] * sw);
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) red[wave][j][r][lane] = acc[j][r];
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < 16 * kDec2Cols; idx += 64 * kDecWaves) {
-      const int ln = idx & 63, j = (idx >> 6) & 3, r = idx >> 8;
-      float o = 0.f;
-#pragma unroll
-      for (int w = 0; w < kDecWaves; w++) o += red[w][j][r][ln];
-      const int row = m0 + (ln >> 4) * 4 + r;
+    for (int r = 0; r < 4; r++) {
+      const int row = 4 * kg + r;
       if (row < M) {
         const int p = row0 + row;
-        obuf[(size_t)p * H + h0 + 16 * j + (ln & 15)] = o * pl.perm_w[p];
+        obuf[((size_t)p * S + du.s) * H + cg * 16 + lr] = acc[r] * pl.perm_w[p];
       }
     }
-    __syncthreads();
   }
-
 }
 
-void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* cbuf, int n_slots, hipStream_t stream) {
-  if (n_slots <= 0) return;
-  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(pb.I / kDec1Cols, n_slots), dim3(64 * kDecWaves), 0, stream,
-                     pb, pl, cbuf);
+// Resident capacity of the 4-wave, <= 96-VGPR decode GEMMs, in workgroups, and the
+// number of 16-column groups one workgroup unit covers.
+int decode_grid() { return num_compute_units() * kDecBlocksPerCU; }
+int decode_unit_groups() { return kDecBlockWaves; }
+
+void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, hipStream_t stream) {
+  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(decode_grid()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, gbuf);
 }
 
-void launch_gemm2_decode(const Problem& pb, const Plan& pl, const float* cbuf, float* obuf, int n_slots,
-                         hipStream_t stream) {
-  if (n_slots <= 0) return;
-  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(pb.H / kDec2Cols, n_slots), dim3(64 * kDecWaves), 0, stream, pb, pl,
-                     cbuf, obuf);
+void launch_activation_decode(const Problem& pb, const Plan& pl, const float* gbuf, const CHalf& ch, int pmax,
+                              hipStream_t stream) {
+  const int waves = pmax * (pb.I / kBlock);
+  if (waves <= 0) return;
+  hipLaunchKernelGGL(activation_decode_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, pb.I, pl, gbuf, ch);
+}
+
+void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, hipStream_t stream) {
+  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(decode_grid()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, ch,
+                     obuf);
 }
 
 }  // namespace moefp8

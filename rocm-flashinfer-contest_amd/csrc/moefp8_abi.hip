@@ -26,15 +26,15 @@ int tile_m_for(int64_t T) {
 
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
-  size_t tok_a2, esig, perm_exact, c16;
+  size_t tok_a2, esig, perm_exact, mtiles, c16, c16_scale, gbuf;
   size_t cbuf, c_q, c_plane, c_scale, c_kmax, obuf, total;
-  int64_t pmax, max_mtiles;
+  int64_t pmax, max_mtiles, rows_cap;
 };
 
 static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
 
 static Layout make_layout(int64_t T, int E_local, int H, int I) {
-  Layout L;
+  Layout L = {};
   const int64_t pmax = T * (E_local < kTopK ? E_local : kTopK);
   L.pmax = pmax;
   size_t o = 0;
@@ -55,16 +55,29 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.tok_a2 = take((size_t)T * 4);
   L.esig = take((size_t)E_local * 2 * 4);
   L.perm_exact = take((size_t)pmax);
-  // C between the GEMMs: fp32 [pmax, I] (small T) or, for large T, kMaxTerms e4m3 planes
-  // [pmax, I] + fp32 scales [pmax, I/128] + per-sub-tile term counts
   const int tm = tile_m_for(T);
   L.max_mtiles = (pmax + tm - 1) / tm + E_local;
   L.c_plane = align_up((size_t)pmax * I);
-  const size_t c_f32 = (size_t)pmax * I * 4;
+  if (T <= kDecodeMaxT) {
+    // small T: m-tile table, GEMM1 partials [rows][2I] fp32, C as f16 hi/lo planes + scales,
+    // GEMM2 partials [rows][H] fp32; rows = pairs x K-split <= rows_cap
+    const int64_t r8 = 8 * pmax < 1024 ? 8 * pmax : 1024;
+    L.rows_cap = pmax > r8 ? pmax : r8;
+    L.mtiles = take((size_t)L.max_mtiles * 16);
+    L.gbuf = take((size_t)L.rows_cap * 2 * I * 4);
+    L.c16 = take(L.c_plane * 2 * 2);
+    L.c16_scale = take((size_t)pmax * (I / kBlock) * 4);
+    L.obuf = take((size_t)L.rows_cap * H * 4);
+    L.total = o;
+    return L;
+  }
+  // large T: kMaxTerms e4m3 planes of C [pmax, I] + fp32 scales [pmax, I/128] + per-sub-tile
+  // term counts, the f16 split of exact-product sub-tiles, and O [pmax][H] fp32
+  L.rows_cap = pmax;
   const size_t c_scale_bytes = align_up((size_t)pmax * (I / kBlock) * 4);
   const size_t c_kmax_bytes = (size_t)L.max_mtiles * (tm / 16) * (I / kBlock);
   const size_t c_split = L.c_plane * kMaxTerms + c_scale_bytes + c_kmax_bytes;
-  L.cbuf = take(c_f32 > c_split ? c_f32 : c_split);
+  L.cbuf = take(c_split);
   L.c_q = L.cbuf;
   L.c_scale = L.c_q + L.c_plane * kMaxTerms;
   L.c_kmax = L.c_scale + c_scale_bytes;
@@ -220,6 +233,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pl.mtile_offsets = reinterpret_cast<int*>(ws + L.mtile_offsets);
   pl.info = reinterpret_cast<int*>(ws + L.info);
   pl.exact = ws + L.perm_exact;
+  pl.mtiles = nullptr;
   float* tok_a2 = reinterpret_cast<float*>(ws + L.tok_a2);
   float* esig = reinterpret_cast<float*>(ws + L.esig);
 
@@ -243,23 +257,31 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   MagInputs mag = {a->hidden_states, a->hidden_states_scale, a->gemm1_weights_scale, a->gemm2_weights_scale,
                    H, I, E_local, tok_a2, esig};
   if (T <= kDecodeMaxT) {
-    // small T: routing (+ scale estimates), permutation, GEMM1, GEMM2, combine
+    // small T: routing (+ scale estimates), permutation, GEMM1, activation, GEMM2, combine
+    const int slots = decode_grid(), groups = decode_unit_groups();
+    const SplitPolicy sp = {slots, 2 * I / (16 * groups), H / kBlock, (int)L.rows_cap,
+                            slots, H / (16 * groups),     I / kBlock, (int)L.rows_cap};
+    pl.mtiles = reinterpret_cast<const int4*>(ws + L.mtiles);
     mark(0);
     launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,
                  topk_ids, topk_w, &mag, s);
     mark(1);
-    launch_permute_small(topk_ids, topk_w, (int)T, E_local, a->local_expert_offset, tile_m,
+    launch_permute_small(topk_ids, topk_w, (int)T, E_local, a->local_expert_offset,
                          const_cast<int*>(pl.expert_offsets), const_cast<int*>(pl.perm_token),
                          const_cast<float*>(pl.perm_w), const_cast<int*>(pl.tok_slot), const_cast<int*>(pl.active),
                          const_cast<int*>(pl.mtile_offsets), const_cast<int*>(pl.info), tok_a2, esig, I,
-                         const_cast<uint8_t*>(pl.exact), s);
+                         const_cast<uint8_t*>(pl.exact), const_cast<int4*>(pl.mtiles), sp, s);
     mark(2);
-    const int n_slots = (int)(L.pmax < E_local ? L.pmax : E_local);
-    float* cbuf = reinterpret_cast<float*>(ws + L.cbuf);
+    float* gbuf = reinterpret_cast<float*>(ws + L.gbuf);
     float* obuf = reinterpret_cast<float*>(ws + L.obuf);
-    launch_gemm1_decode(pb, pl, cbuf, n_slots, s);
+    CHalf ch;
+    ch.hi = reinterpret_cast<_Float16*>(ws + L.c16);
+    ch.lo = ch.hi + L.c_plane;
+    ch.scale = reinterpret_cast<float*>(ws + L.c16_scale);
+    launch_gemm1_decode(pb, pl, gbuf, s);
+    launch_activation_decode(pb, pl, gbuf, ch, (int)L.pmax, s);
     mark(3);
-    launch_gemm2_decode(pb, pl, cbuf, obuf, n_slots, s);
+    launch_gemm2_decode(pb, pl, ch, obuf, s);
     mark(4);
     launch_combine(pl, obuf, a->output, (int)T, H, s);
     mark(5);

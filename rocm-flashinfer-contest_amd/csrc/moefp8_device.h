@@ -71,11 +71,26 @@ __device__ __forceinline__ void split_f16(float x, float inv, _Float16& hi, _Flo
 // rms(C) ~ 0.7 rms(G1)^2, rms(O) ~ rms(C) s2 sqrt(I).
 constexpr float kPreciseRms = 96.0f;
 
+// Per-pair flag bits.  The small-T GEMM2 multiplies C's f16 hi term alone (relative
+// error 2^-11 per element, ~2^-12 rms of the output) unless the predicted output rms
+// exceeds kOneTermRms; the predictor overestimates the measured rms about 7x.
+constexpr float kOneTermRms = 8.0f;
+constexpr uint8_t kFlagExactProducts = 1;
+constexpr uint8_t kFlagTwoTermC = 2;
+
+__device__ __forceinline__ float predicted_output_rms(float a2, float w, float s13, float s2, float sqrt_i) {
+  return fabsf(w) * 0.7f * a2 * s13 * s13 * s2 * sqrt_i;
+}
+
 __device__ __forceinline__ bool needs_exact_products(float a2, float w, float s13, float s2, float sqrt_i) {
-  return fabsf(w) * 0.7f * a2 * s13 * s13 * s2 * sqrt_i > kPreciseRms;
+  return predicted_output_rms(a2, w, s13, s2, sqrt_i) > kPreciseRms;
 }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+// A value the caller knows to be equal on every lane, moved to a scalar register.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// Wavefront index inside the workgroup, as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_index() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
 __device__ __forceinline__ int shfl_xor_i(int v, int m) { return __shfl_xor(v, m, kWave); }

@@ -17,6 +17,13 @@ struct MagInputs {
   float* esig;     // [E, 2] rms estimates of W13 and W2 entries
 };
 
+// K-split choice of the small-T GEMMs: the largest S in {8, 4, 2, 1} with
+// m_tiles * ncb * S <= slots, S * P <= rows_cap and S <= kb.
+struct SplitPolicy {
+  int slots1, ncb1, kb1, rows_cap1;   // GEMM1: grid workgroups, column blocks per m-tile, K-blocks (H/128)
+  int slots2, ncb2, kb2, rows_cap2;   // GEMM2: the same for H columns and I/128 K-blocks
+};
+
 // Routing of every token (main.py:139-165): topk_ids [T,8] ascending, topk_w [T,8];
 // with `mag`, also the magnitude estimates.
 void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
@@ -29,11 +36,12 @@ void launch_permute(const int* topk_ids, const float* topk_w, int T, int E_local
                     int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
                     uint8_t* perm_exact, hipStream_t stream);
 
-// The same permutation for T <= 64 in one workgroup with no serial loop.
-void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset, int tile_m,
+// The same permutation for T <= 64 in one workgroup with no serial loop, plus the
+// m-tile table (tile height 16) and the K-splits of the small-T GEMMs.
+void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset,
                           int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
                           int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
-                          uint8_t* perm_exact, hipStream_t stream);
+                          uint8_t* perm_exact, int4* mtiles, const SplitPolicy& sp, hipStream_t stream);
 
 // Pointers into the caller's workspace produced by routing + permutation.
 struct Plan {
@@ -43,8 +51,9 @@ struct Plan {
   const int* tok_slot;        // [T * 8]
   const int* active;          // [E_local]
   const int* mtile_offsets;   // [E_local + 1]
-  const int* info;            // {P, n_active, m_tiles}
+  const int* info;            // {P, n_active, m_tiles, S1, S2}: S1/S2 = K-splits of the small-T GEMMs
   const uint8_t* exact;       // [Pmax] 1 = pair runs on the exact-product (f16 MFMA) path
+  const int4* mtiles;         // small T: per m-tile {expert, first pair, rows, 0}
 };
 
 struct Problem {
@@ -57,12 +66,18 @@ struct Problem {
   int T, E_local, H, I;
 };
 
-// Small-T path: weight-streaming GEMM1 (+SwiGLU, fp32 C) and GEMM2 (quantise C on load).
-void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* cbuf, int n_slots, hipStream_t stream);
-// GEMM2 for small T: workgroup = (active expert, 64 H columns), 8 waves split K.
-constexpr int kDec2Cols = 64;
-void launch_gemm2_decode(const Problem& pb, const Plan& pl, const float* cbuf, float* obuf, int n_slots,
-                         hipStream_t stream);
+// Small-T path: GEMM1 partials -> activation (f16 hi/lo C) -> GEMM2 partials.
+struct CHalf {
+  _Float16* hi;   // [Pmax][I]
+  _Float16* lo;   // [Pmax][I]
+  float* scale;   // [Pmax][I/128]
+};
+int decode_grid();
+int decode_unit_groups();
+void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, hipStream_t stream);
+void launch_activation_decode(const Problem& pb, const Plan& pl, const float* gbuf, const CHalf& ch, int pmax,
+                              hipStream_t stream);
+void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, hipStream_t stream);
 
 // GEMM1 -> GEMM2 activations of the large-T path: up to kMaxTerms e4m3 planes of C,
 // one fp32 scale per (pair, 128 columns) and the term count of every 16-row sub-tile.

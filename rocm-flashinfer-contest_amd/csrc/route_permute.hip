@@ -309,6 +309,8 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
     info[0] = run;    // P
     info[1] = n_act;  // active experts
     info[2] = mt;     // m-tiles of height tile_m
+    info[3] = 1;      // K-splits (small-T GEMMs only)
+    info[4] = 1;
   }
   __syncthreads();
 
@@ -377,21 +379,36 @@ __global__ __launch_bounds__(kPermThreads) void permute_kernel(
   }
 }
 
+// Largest K-split S in {8, 4, 2, 1} whose units still fit the grid and the partial rows.
+__device__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap) {
+  for (int S = 8; S > 1; S >>= 1)
+    if ((int64_t)n_mt * ncb * S <= slots && (int64_t)S * P <= rows_cap && S <= kb) return S;
+  return 1;
+}
+
 // Stable permutation for T <= 64 (one workgroup, one thread per (token, k) pair).  A 64-bit
 // LDS mask of the tokens that picked each local expert gives its count (popcount) and each
 // pair's rank inside the expert (popcount of the lower tokens), so pairs come out
 // expert-major and token-ascending as in main.py:218-225 with no serial loop; the offsets
-// are exclusive prefix sums built from one ballot per bit (counts are <= 64).
+// are exclusive prefix sums built from one ballot per bit (counts are <= 64).  Also
+// writes the m-tile table {expert, first pair, rows} (tile height 16) and the GEMM
+// K-splits.
 constexpr int kSmallT = 64;
+constexpr int kSmallTile = 16;
 constexpr int kSmallPermThreads = kSmallT * kTopK;
+constexpr int kSmallMaxMtiles = kSmallPermThreads / kSmallTile + kEGlobal;
 
 __global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
-    const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int E_local, int offset, int tile_m,
+    const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int E_local, int offset,
     int* __restrict__ expert_offsets, int* __restrict__ perm_token, float* __restrict__ perm_w,
     int* __restrict__ tok_slot, int* __restrict__ active, int* __restrict__ mtile_offsets, int* __restrict__ info,
-    const float* __restrict__ tok_a2, const float* __restrict__ esig, float sqrt_i, uint8_t* __restrict__ perm_exact) {
+    const float* __restrict__ tok_a2, const float* __restrict__ esig, float sqrt_i, uint8_t* __restrict__ perm_exact,
+    int4* __restrict__ mtiles, SplitPolicy sp) {
   __shared__ unsigned long long tmask[kEGlobal];
   __shared__ int base_s[kEGlobal];
+  __shared__ int mtb_s[kEGlobal];                   // first m-tile of each local expert
+  __shared__ int4 mt_s[kSmallMaxMtiles];            // {expert, first pair, rows, OR of pair flags}
+  __shared__ int n_mt_s;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   const int t = tid >> 3, j = tid & 7;
   const bool in = t < T;
@@ -413,7 +430,7 @@ __global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
     for (int e0 = 0; e0 < E_local; e0 += kWave) {
       const int e = e0 + lane;
       const int c = e < E_local ? __popcll(tmask[e]) : 0;
-      const int mt = (c + tile_m - 1) / tile_m;
+      const int mt = (c + kSmallTile - 1) / kSmallTile;
       int pc = 0, pm = 0;
 #pragma unroll
       for (int bit = 0; bit < 7; bit++) {
@@ -426,6 +443,9 @@ __global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
         mtile_offsets[e] = carry_mt + pm;
         base_s[e] = carry_p + pc;
         if (c > 0) active[carry_a + lanes_below(act)] = e;
+        mtb_s[e] = carry_mt + pm;
+        for (int j = 0; j < mt; j++)
+          mt_s[carry_mt + pm + j] = int4{e, carry_p + pc + kSmallTile * j, min(kSmallTile, c - kSmallTile * j), 0};
       }
       carry_p += __builtin_amdgcn_readlane(pc + c, kWave - 1);
       carry_mt += __builtin_amdgcn_readlane(pm + mt, kWave - 1);
@@ -436,7 +456,10 @@ __global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
       mtile_offsets[E_local] = carry_mt;
       info[0] = carry_p;    // P
       info[1] = carry_a;    // active experts
-      info[2] = carry_mt;   // m-tiles of height tile_m
+      info[2] = carry_mt;   // m-tiles of height 16
+      info[3] = pick_split(carry_mt, sp.ncb1, sp.kb1, sp.slots1, carry_p, sp.rows_cap1);
+      info[4] = pick_split(carry_mt, sp.ncb2, sp.kb2, sp.slots2, carry_p, sp.rows_cap2);
+      n_mt_s = carry_mt;
     }
   }
   __syncthreads();
@@ -449,19 +472,24 @@ __global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
     const int pos = base_s[le] + (int)__popcll(tmask[le] & ((1ull << t) - 1ull));
     perm_token[pos] = t;
     perm_w[pos] = w;
-    perm_exact[pos] = needs_exact_products(a2, w, esig[2 * le], esig[2 * le + 1], sqrt_i);
+    const float pred = predicted_output_rms(a2, w, esig[2 * le], esig[2 * le + 1], sqrt_i);
+    const int flags = (pred > kPreciseRms ? kFlagExactProducts : 0) | (pred > kOneTermRms ? kFlagTwoTermC : 0);
+    perm_exact[pos] = (uint8_t)flags;
     tok_slot[t * kTopK + k] = pos;
+    if (flags) atomicOr(&mt_s[mtb_s[le] + (pos - base_s[le]) / kSmallTile].w, flags);
   }
   if (in && j >= n) tok_slot[t * kTopK + j] = -1;
+  __syncthreads();
+  for (int g = tid; g < n_mt_s; g += kSmallPermThreads) mtiles[g] = mt_s[g];
 }
 
-void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset, int tile_m,
+void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset,
                           int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
                           int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
-                          uint8_t* perm_exact, hipStream_t stream) {
+                          uint8_t* perm_exact, int4* mtiles, const SplitPolicy& sp, hipStream_t stream) {
   hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(kSmallPermThreads), 0, stream, topk_ids, topk_w, T,
-                     E_local, offset, tile_m, expert_offsets, perm_token, perm_w, tok_slot, active, mtile_offsets,
-                     info, tok_a2, esig, sqrtf((float)I), perm_exact);
+                     E_local, offset, expert_offsets, perm_token, perm_w, tok_slot, active, mtile_offsets, info,
+                     tok_a2, esig, sqrtf((float)I), perm_exact, mtiles, sp);
 }
 
 void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
