@@ -1,0 +1,71 @@
+// Combine (main.py:241-243): each token's pair rows, summed in ascending expert order
+// starting from zero (the order of index_add_ in the reference), rounded once to bf16.
+// Tokens without a local expert get exact zero rows.  Pair rows may come split over K
+// (small-T GEMM2); the splits of a pair are added first, in ascending order.
+#include "moefp8_device.h"
+#include "moefp8_launch.h"
+
+namespace moefp8 {
+
+// Workgroup = (token, 1024 columns), 4 columns per thread.
+constexpr int kCombineCols = 1024;
+
+__global__ __launch_bounds__(256) void combine_kernel(const int* __restrict__ tok_slot,
+                                                      const int* __restrict__ info,
+                                                      const float* __restrict__ obuf,
+                                                      uint16_t* __restrict__ out, int H) {
+  const int t = blockIdx.x;
+  const int c = blockIdx.y * kCombineCols + 4 * threadIdx.x;
+  const int S = info[4];
+  int slots[kTopK];
+#pragma unroll
+  for (int k = 0; k < kTopK; k++) slots[k] = tok_slot[(size_t)t * kTopK + k];
+  if (c >= H) return;
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (S == 1) {
+    float4 v[kTopK];
+#pragma unroll
+    for (int k = 0; k < kTopK; k++)
+      v[k] = slots[k] >= 0 ? *reinterpret_cast<const float4*>(obuf + (size_t)slots[k] * H + c)
+                           : float4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < kTopK; k++) {
+      if (slots[k] < 0) break;
+      acc.x += v[k].x;
+      acc.y += v[k].y;
+      acc.z += v[k].z;
+      acc.w += v[k].w;
+    }
+  } else {
+    // K-split partials of each pair row, added split by split, then pair by pair
+    for (int k = 0; k < kTopK; k++) {
+      if (slots[k] < 0) break;
+      const float* row = obuf + (size_t)slots[k] * S * H + c;
+      float4 o = *reinterpret_cast<const float4*>(row);
+      for (int s = 1; s < S; s++) {
+        const float4 v = *reinterpret_cast<const float4*>(row + (size_t)s * H);
+        o.x += v.x;
+        o.y += v.y;
+        o.z += v.z;
+        o.w += v.w;
+      }
+      acc.x += o.x;
+      acc.y += o.y;
+      acc.z += o.z;
+      acc.w += o.w;
+    }
+  }
+  uint2 o;
+  o.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
+  o.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
+  *reinterpret_cast<uint2*>(out + (size_t)t * H + c) = o;
+}
+
+
+void launch_combine(const Plan& pl, const float* obuf, uint16_t* out, int T, int H, hipStream_t stream) {
+  if (T <= 0) return;
+  hipLaunchKernelGGL(combine_kernel, dim3(T, (H + kCombineCols - 1) / kCombineCols), dim3(256), 0, stream,
+                     pl.tok_slot, pl.info, obuf, out, H);
+}
+
+}  // namespace moefp8

@@ -1,0 +1,575 @@
+// Grouped expert GEMMs for T > 64 (prefill): LDS-staged activations, per-wavefront
+// weight streams.
+//
+// A workgroup of 4 wavefronts owns one unit = (m-block of BM = 16*MT rows of one expert,
+// block of 128 output columns).  Each wavefront streams its own 32 or 64 weight rows
+// straight from HBM into a 2-deep register ring (no sharing needed: no other wavefront
+// of the workgroup uses them) and keeps MT x NT 16x16 accumulators.  The BM activation
+// rows, shared by all 4 wavefronts, are copied HBM/L2 -> LDS by DMA (global_load_lds,
+// no registers) into a 3-stage ring one K-block per stage, together with their per-row
+// scales.  LDS operand reads are issued as inline ds_read_b128 together with their
+// lgkmcnt wait: the compiler cannot prove that an LDS read does not alias a DMA in
+// flight to another stage and would otherwise drain every outstanding load before it.
+// Every wavefront issues the same number of memory operations per K-block, so one
+// vmcnt wait (explicit count) plus s_barrier per K-block publishes the stage.
+//
+// Block scales are applied per 128-K block in fp32: acc += MFMA(A_kb, B_kb) * sa[row] * sw.
+//
+// GEMM1  G1 = A_e W13_e^T on the e4m3 MFMA (m-blocks holding a pair flagged for exact
+//        products: f16 MFMA on widened operands), SwiGLU in the epilogue (main.py:229-233),
+//        and C written as hi = f16(C/s), s = max|C row block| / 448 per 128 cols, plus a lo
+//        term: e4m3(2^11 (C/s - hi)) (about 15 significant bits in all), or f16(C/s - hi)
+//        (22 bits) in m-blocks with exact-product pairs, whose outputs reach 1e4 and may
+//        cancel in the per-token sum.
+// GEMM2  O = C W2_e^T (main.py:234-238): C's hi term on the f16 MFMA against W2 widened
+//        to f16 (exact products, 2^-11 relative input error); m-blocks holding a pair that
+//        needs more add the e4m3 lo term on the scaled e4m3 MFMA (2^-11), or the f16 lo term
+//        on the f16 MFMA.  Rows are scaled by the routing weight (main.py:240) and summed per
+//        token by the combine kernel.
+#include "moefp8_device.h"
+#include "moefp8_launch.h"
+
+namespace moefp8 {
+
+constexpr int kLgWaves = 4;
+constexpr int kLgThreads = 64 * kLgWaves;
+constexpr int kLgDepth = 2;                  // weight K-blocks in flight per wavefront
+constexpr int kLgStages = kLgDepth + 1;      // activation stages in LDS
+constexpr float kLoScale = 2048.0f;          // lo term of C is stored x 2^11
+
+template <int kCount>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(kCount >= 0 && kCount < 64, "vmcnt range");
+  // gfx9 s_waitcnt encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14
+  __builtin_amdgcn_s_waitcnt((kCount & 15) | (7 << 4) | (15 << 8) | ((kCount >> 4) << 14));
+}
+
+// LDS operand reads and their completion wait in one asm statement: the results are defined
+// only after the wait, so the compiler can place nothing (e.g. a register copy) that reads
+// a destination register while its LDS read is still in flight.
+__device__ __forceinline__ void lds_read3(uint32_t a0, uint32_t a1, uint32_t a2, v4i& r0, v4i& r1, v4i& r2) {
+  asm volatile(
+      "ds_read_b128 %0, %3\n\t"
+      "ds_read_b128 %1, %4\n\t"
+      "ds_read_b128 %2, %5\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2)
+      : "v"(a0), "v"(a1), "v"(a2)
+      : "memory");
+}
+__device__ __forceinline__ void lds_read2(uint32_t a0, uint32_t a1, v4i& r0, v4i& r1) {
+  asm volatile(
+      "ds_read_b128 %0, %2\n\t"
+      "ds_read_b128 %1, %3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1)
+      : "v"(a0), "v"(a1)
+      : "memory");
+}
+__device__ __forceinline__ void lds_read4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, v4i& r0, v4i& r1,
+                                          v4i& r2, v4i& r3) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %5\n\t"
+      "ds_read_b128 %2, %6\n\t"
+      "ds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "memory");
+}
+__device__ __forceinline__ void lds_read5(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, uint32_t a4, v4i& r0,
+                                          v4i& r1, v4i& r2, v4i& r3, v4i& r4) {
+  asm volatile(
+      "ds_read_b128 %0, %5\n\t"
+      "ds_read_b128 %1, %6\n\t"
+      "ds_read_b128 %2, %7\n\t"
+      "ds_read_b128 %3, %8\n\t"
+      "ds_read_b128 %4, %9\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3), "=&v"(r4)
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(a4)
+      : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
+
+// Wave-uniform read of kernel-constant data through the constant address space, so the
+// compiler can use a scalar load (counted by lgkmcnt, not by the vmcnt pipeline above).
+__device__ __forceinline__ float load_uniform(const float* p) {
+  return *(const __attribute__((address_space(4))) float*)p;
+}
+
+__device__ __forceinline__ v8i load_w(const uint8_t* p) {
+  const v4i* q = reinterpret_cast<const v4i*>(p);
+  const v4i x = q[0], y = q[1];
+  return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__device__ __forceinline__ v8i cat(v4i x, v4i y) { return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7); }
+
+__device__ __forceinline__ v8h as_v8h(v4i x) { return __builtin_bit_cast(v8h, x); }
+
+// e4m3 MFMA with A scaled by 2^(e - 127) exactly.
+template <int kExp>
+__device__ __forceinline__ v4f mfma16x16x128_exp(const v8i& a, const v8i& b, const v4f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, kExp, 0, 127);
+}
+
+// ------------------------------------------------------------------------------------------ GEMM1
+// LDS stage: MT m-tiles x [8 chunks of 16 B][16 rows][16 B] of e4m3 activations, then 4 x 64
+// row scales (one slot per wavefront; rows >= BM are padding).
+template <int MT>
+struct G1L {
+  static constexpr int kA = MT * 2048;
+  static constexpr int kStage = kA + kLgWaves * 64 * 4;
+  static constexpr int kDmaA = MT / 2;                 // 1 KB activation DMAs per wave per K-block
+  static constexpr int kOps = kDmaA + 1 + 8;           // + row-scale DMA + 4 weight tiles x 2 loads
+};
+
+// One pass over K for m-tiles [i0, i0 + NA) of the unit's m-block (the DMA always stages all
+// MT m-tiles, so every pass issues the same operations).  kExact: the pass runs on the f16
+// MFMA with widened operands (exact products).
+//
+// Every m-tile of the pass is computed, also past the block's last row (those rows hold
+// clamped copies and are never stored): a K step is straight-line code with no branch between
+// an MFMA and the VALU instructions that read its result.  The compiler's hazard check does
+// not count the wait states of an MFMA in a conditional block correctly for a reader in a
+// later block (a scaled 16x16x128 MFMA needs 12, it inserted 8), and the reader then sees
+// the register's previous contents.
+template <int MT, int NA, bool kExact>
+__device__ __forceinline__ void gemm1_large_pass(const Problem& pb, const Plan& pl, uint8_t* ring, int e, int row0,
+                                                 int rows, int cb, int i0, v4f (&acc)[NA][4]) {
+  using L = G1L<MT>;
+  const int H = pb.H, I = pb.I, T = pb.T, KB = H / kBlock, NCB = I / kBlock;
+  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  const int col0 = cb * kBlock + 32 * wave;
+  const uint8_t* bp = pb.w13 + ((size_t)e * 2 * I + col0 + lr) * H + kg * 32;
+  const size_t gate_off = (size_t)I * H;
+  const float* swu = pb.s13 + ((size_t)e * (2 * I / kBlock) + cb) * KB;
+  const float* swg = swu + (size_t)NCB * KB;
+  // activation DMA sources: wave w carries m-tiles (w/2) + 2r, chunk half w%2
+  const uint8_t* asrc[L::kDmaA];
+#pragma unroll
+  for (int r = 0; r < L::kDmaA; r++) {
+    const int row = 16 * ((wave >> 1) + 2 * r) + lr;
+    const int tok = pl.perm_token[row0 + min(row, rows - 1)];
+    asrc[r] = pb.hidden + (size_t)tok * H + (4 * (wave & 1) + kg) * 16;
+  }
+  const int srow = min(64 * wave + lane, rows - 1);
+  const float* ssrc = pb.hscale + pl.perm_token[row0 + srow];
+#pragma unroll
+  for (int i = 0; i < NA; i++)
+#pragma unroll
+    for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
+  v8i B[kLgDepth][4];
+  float SU[kLgDepth], SG[kLgDepth];
+
+  auto issue = [&](int d, int j) {
+    const int k = min(j, KB - 1);
+    uint8_t* st = ring + (j % kLgStages) * L::kStage;
+#pragma unroll
+    for (int r = 0; r < L::kDmaA; r++)
+      __builtin_amdgcn_global_load_lds(asrc[r] + (size_t)k * kBlock,
+                                       st + (((wave >> 1) + 2 * r) * 2048 + (wave & 1) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(ssrc + (size_t)k * T, st + L::kA + wave * 256, 4, 0, 0);
+    const uint8_t* b = bp + (size_t)k * kBlock;
+    B[d][0] = load_w(b);
+    B[d][1] = load_w(b + (size_t)16 * H);
+    B[d][2] = load_w(b + gate_off);
+    B[d][3] = load_w(b + gate_off + (size_t)16 * H);
+    SU[d] = load_uniform(swu + k);
+    SG[d] = load_uniform(swg + k);
+  };
+  auto step = [&](int d, int j) {
+    // at most the operations of the following kLgDepth - 1 steps may still be in flight
+    // (every wavefront issues at least L::kOps vector-memory operations per step)
+    wait_vmcnt<(kLgDepth - 1) * L::kOps>();
+    __builtin_amdgcn_s_barrier();
+    const uint8_t* st = ring + (j % kLgStages) * L::kStage;
+#pragma unroll
+    for (int ia = 0; ia < NA; ia++) {
+      const int i = i0 + ia;
+      v4i x, y, s4;
+      lds_read3(lds_addr(st + i * 2048 + ((2 * kg) * 16 + lr) * 16),
+                lds_addr(st + i * 2048 + ((2 * kg + 1) * 16 + lr) * 16), lds_addr(st + L::kA + (16 * i + 4 * kg) * 4),
+                x, y, s4);
+      const v8i a = cat(x, y);
+      const float4 sa = __builtin_bit_cast(float4, s4);
+      if constexpr (!kExact) {
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+          const float sw = n < 2 ? SU[d] : SG[d];
+          const v4f p = mfma16x16x128(a, B[d][n], v4f{0.f, 0.f, 0.f, 0.f});
+          acc[ia][n][0] += p[0] * (sa.x * sw);
+          acc[ia][n][1] += p[1] * (sa.y * sw);
+          acc[ia][n][2] += p[2] * (sa.z * sw);
+          acc[ia][n][3] += p[3] * (sa.w * sw);
+        }
+      } else {
+        v8h a16[4];
+        widen_fp8_operand(a, a16);
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+          const float sw = n < 2 ? SU[d] : SG[d];
+          v8h b16[4];
+          widen_fp8_operand(B[d][n], b16);
+          const v4f p = mfma_f16_block(a16, b16, v4f{0.f, 0.f, 0.f, 0.f});
+          acc[ia][n][0] += p[0] * (sa.x * sw);
+          acc[ia][n][1] += p[1] * (sa.y * sw);
+          acc[ia][n][2] += p[2] * (sa.z * sw);
+          acc[ia][n][3] += p[3] * (sa.w * sw);
+        }
+      }
+    }
+    // stage (j + kLgDepth) % kLgStages was last read at step j - 1, before this barrier
+    issue(d, j + kLgDepth);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // the previous pass's LDS reads are complete before its stages are refilled
+  __syncthreads();
+  // stage d's operations must all be issued before stage d + 1's: the per-step vmcnt wait
+  // counts operations in issue order
+#pragma unroll
+  for (int d = 0; d < kLgDepth; d++) {
+    issue(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  int j = 0;
+  for (; j + 2 * kLgDepth <= KB; j += 2 * kLgDepth) {
+#pragma unroll
+    for (int d = 0; d < 2 * kLgDepth; d++) step(d % kLgDepth, j + d);
+  }
+  for (; j < KB; j += kLgDepth) {
+#pragma unroll
+    for (int d = 0; d < kLgDepth; d++)
+      if (j + d < KB) step(d, j + d);
+  }
+  // no DMA may still target the ring when the next pass refills it or the workgroup ends
+  wait_vmcnt<0>();
+}
+
+// Epilogue of m-tiles [i0, i0 + NA): C = silu(gate) * up and its split.  amax_s holds, per
+// wavefront and row, the largest |C| of the wavefront's 32 columns.  kLo16 (m-blocks with
+// exact-product pairs): the lo term is f16(C/s - hi), 22 significant bits in all, instead of
+// the e4m3 2^11 (C/s - hi).
+template <int MT, int NA, bool kLo16>
+__device__ __forceinline__ void gemm1_large_store(const Plan& pl, const CHalf8& ch, float (*amax_s)[16 * MT], int I,
+                                                  int row0, int rows, int cb, int i0, const v4f (&acc)[NA][4]) {
+  const int NCB = I / kBlock;
+  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  const int col0 = cb * kBlock + 32 * wave;
+  float c[NA][2][4];
+#pragma unroll
+  for (int ia = 0; ia < NA; ia++)
+#pragma unroll
+    for (int jn = 0; jn < 2; jn++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) c[ia][jn][r] = silu_f32(acc[ia][jn + 2][r]) * acc[ia][jn][r];
+#pragma unroll
+  for (int ia = 0; ia < NA; ia++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float m = fmaxf(fabsf(c[ia][0][r]), fabsf(c[ia][1][r]));
+      m = fmaxf(m, dpp_f32<kDppXor1>(m));
+      m = fmaxf(m, dpp_f32<kDppXor2>(m));
+      m = fmaxf(m, dpp_f32<kDppHalfMirror>(m));
+      m = fmaxf(m, dpp_f32<kDppRowMirror>(m));
+      if (lr == 0) amax_s[wave][16 * (i0 + ia) + 4 * kg + r] = m;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int ia = 0; ia < NA; ia++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int row = 16 * (i0 + ia) + 4 * kg + r;
+      if (row >= rows) continue;
+      const float amax = fmaxf(fmaxf(amax_s[0][row], amax_s[1][row]), fmaxf(amax_s[2][row], amax_s[3][row]));
+      float inv, scale;
+      split_scale(amax, inv, scale);
+      const size_t p = (size_t)(row0 + row);
+#pragma unroll
+      for (int jn = 0; jn < 2; jn++) {
+        const int col = col0 + 16 * jn + lr;
+        const float v = fminf(fmaxf(c[ia][jn][r] * inv, -448.0f), 448.0f);
+        const _Float16 hi = (_Float16)v;
+        ch.hi[p * I + col] = hi;
+        if constexpr (kLo16) ch.lo16[p * I + col] = (_Float16)(v - (float)hi);
+        else ch.lo[p * I + col] = (uint8_t)f32_to_e4m3(fminf(fmaxf((v - (float)hi) * kLoScale, -448.0f), 448.0f));
+      }
+      if (wave == 0 && lr == 0) ch.scale[p * NCB + cb] = scale;
+    }
+  }
+  // amax_s is rewritten by the next store
+  __syncthreads();
+}
+
+template <int MT>
+__global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, Plan pl, CHalf8 ch) {
+  using L = G1L<MT>;
+  static_assert(MT % 2 == 0, "two activation DMAs per m-tile");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
+  __shared__ float amax_s[kLgWaves][16 * MT];
+  const int I = pb.I, NCB = I / kBlock;
+  const int n_units = pl.info[2] * NCB;
+
+  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const int mb = u / NCB, cb = u - mb * NCB;
+    const int4 blk = pl.mblocks1[mb];
+    const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), mt0 = uniform(blk.w);
+    const int mvalid = (rows + 15) / 16;
+    int any_exact = 0;
+#pragma unroll
+    for (int i = 0; i < MT; i++) any_exact |= i < mvalid ? pl.mt_flags[mt0 + i] & kFlagExactProducts : 0;
+    if (!uniform(any_exact)) {
+      v4f acc[MT][4];
+      gemm1_large_pass<MT, MT, false>(pb, pl, ring, e, row0, rows, cb, 0, acc);
+      gemm1_large_store<MT, MT, false>(pl, ch, amax_s, I, row0, rows, cb, 0, acc);
+    } else {
+      // rare: two m-tiles per pass over K, with exact products (the f16 MFMA on widened
+      // operands needs the registers of the fp8 path twice over)
+      for (int i0 = 0; i0 < mvalid; i0 += 2) {
+        v4f acc[2][4];
+        gemm1_large_pass<MT, 2, true>(pb, pl, ring, e, row0, rows, cb, i0, acc);
+        gemm1_large_store<MT, 2, true>(pl, ch, amax_s, I, row0, rows, cb, i0, acc);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------ GEMM2
+// Modes of an m-block, from the flags of its m-tiles: one term (C's hi only), two terms (hi and
+// the e4m3 lo term, MT m-tiles per pass), precise (hi and the f16 lo term, MT/2 m-tiles per
+// pass so that both f16 planes fit the same stage).
+constexpr int kOneTerm = 0, kTwoTerms = 1, kPrecise = 2;
+
+// LDS stage: [hi: MT x 4096 B][lo: MT x 2048 B][4 x 64 row scales].  An m-tile's hi (and f16
+// lo) term is [16 chunks of 16 B][16 rows][16 B]; its e4m3 lo term is [8 chunks][16 rows][16 B].
+// The precise mode puts its NP = MT/2 m-tiles of hi at 0 and of f16 lo at NP x 4096.
+template <int MT>
+struct G2L {
+  static constexpr int kHi = MT * 4096;
+  static constexpr int kLo = MT * 2048;
+  static constexpr int kScales = kHi + kLo;
+  static constexpr int kStage = kScales + kLgWaves * 64 * 4;
+};
+
+// Vector-memory operations per wavefront and K step: hi DMAs (one 1 KB quarter of each m-tile),
+// lo DMAs, the row-scale DMA and 2 weight tiles x 2 loads.
+template <int NP, int kMode>
+constexpr int g2_ops() {
+  return NP + (kMode == kTwoTerms ? NP / 2 : kMode == kPrecise ? NP : 0) + 1 + 4;
+}
+
+// One pass over K for m-tiles [i0, i0 + NP) of the unit's m-block.  As in GEMM1, every m-tile
+// of the pass is computed and a K step has no branch between an MFMA and the instructions that
+// read its result.
+template <int MT, int NP, int kMode>
+__device__ __forceinline__ void gemm2_large_pass(const Problem& pb, const CHalf8& ch, uint8_t* ring, int e, int row0,
+                                                 int rows, int hb, int i0, v4f (&acc)[NP][2]) {
+  using L = G2L<MT>;
+  static_assert(kMode != kTwoTerms || NP % 2 == 0, "e4m3 lo DMA carries two m-tiles per wavefront pair");
+  constexpr int kLoDma = kMode == kTwoTerms ? NP / 2 : kMode == kPrecise ? NP : 0;
+  const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock;
+  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  const uint8_t* bp = pb.w2 + ((size_t)e * H + hb * kBlock + 32 * wave + lr) * I + kg * 32;
+  const float* swp = pb.s2 + ((size_t)e * HB + hb) * KB;
+  // hi (and f16 lo) DMA: wave w carries quarter w of every m-tile; e4m3 lo DMA: m-tiles
+  // (w/2) + 2r, half w%2
+  const _Float16* hsrc[NP];
+#pragma unroll
+  for (int i = 0; i < NP; i++) {
+    const int p = row0 + min(16 * (i0 + i) + lr, rows - 1);
+    hsrc[i] = ch.hi + (size_t)p * I + (4 * wave + kg) * 8;
+  }
+  const uint8_t* lsrc[kLoDma > 0 ? kLoDma : 1];
+#pragma unroll
+  for (int r = 0; r < kLoDma; r++) {
+    if constexpr (kMode == kTwoTerms) {
+      const int p = row0 + min(16 * (i0 + (wave >> 1) + 2 * r) + lr, rows - 1);
+      lsrc[r] = ch.lo + (size_t)p * I + (4 * (wave & 1) + kg) * 16;
+    } else {
+      const int p = row0 + min(16 * (i0 + r) + lr, rows - 1);
+      lsrc[r] = reinterpret_cast<const uint8_t*>(ch.lo16 + (size_t)p * I + (4 * wave + kg) * 8);
+    }
+  }
+  const float* ssrc = ch.scale + (size_t)(row0 + min(16 * i0 + 64 * wave + lane, rows - 1)) * KB;
+
+  v8i B[kLgDepth][2];
+  float SW[kLgDepth];
+  auto issue = [&](int d, int j) {
+    const int k = min(j, KB - 1);
+    uint8_t* st = ring + (j % kLgStages) * L::kStage;
+#pragma unroll
+    for (int i = 0; i < NP; i++)
+      __builtin_amdgcn_global_load_lds(hsrc[i] + (size_t)k * kBlock, st + i * 4096 + wave * 1024, 16, 0, 0);
+#pragma unroll
+    for (int r = 0; r < kLoDma; r++) {
+      if constexpr (kMode == kTwoTerms)
+        __builtin_amdgcn_global_load_lds(lsrc[r] + (size_t)k * kBlock,
+                                         st + L::kHi + ((wave >> 1) + 2 * r) * 2048 + (wave & 1) * 1024, 16, 0, 0);
+      else
+        __builtin_amdgcn_global_load_lds(lsrc[r] + (size_t)k * kBlock * 2, st + (NP + r) * 4096 + wave * 1024, 16,
+                                         0, 0);
+    }
+    __builtin_amdgcn_global_load_lds(ssrc + k, st + L::kScales + wave * 256, 4, 0, 0);
+    const uint8_t* b = bp + (size_t)k * kBlock;
+    B[d][0] = load_w(b);
+    B[d][1] = load_w(b + (size_t)16 * I);
+    SW[d] = load_uniform(swp + k);
+  };
+  auto step = [&](int d, int j) {
+    // at most the operations of the following kLgDepth - 1 steps may still be in flight
+    wait_vmcnt<(kLgDepth - 1) * g2_ops<NP, kMode>()>();
+    __builtin_amdgcn_s_barrier();
+    const uint8_t* st = ring + (j % kLgStages) * L::kStage;
+    v8h b16[2][4];
+    widen_fp8_operand(B[d][0], b16[0]);
+    widen_fp8_operand(B[d][1], b16[1]);
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+      const uint8_t* ti = st + i * 4096;
+      v4i h0, h1, h2, h3, s4;
+      lds_read5(lds_addr(ti + ((4 * kg + 0) * 16 + lr) * 16), lds_addr(ti + ((4 * kg + 1) * 16 + lr) * 16),
+                lds_addr(ti + ((4 * kg + 2) * 16 + lr) * 16), lds_addr(ti + ((4 * kg + 3) * 16 + lr) * 16),
+                lds_addr(st + L::kScales + (16 * i + 4 * kg) * 4), h0, h1, h2, h3, s4);
+      const v8h ah[4] = {as_v8h(h0), as_v8h(h1), as_v8h(h2), as_v8h(h3)};
+      const float4 sa = __builtin_bit_cast(float4, s4);
+      v8i al = {};
+      v8h al16[4] = {};
+      if constexpr (kMode == kTwoTerms) {
+        v4i x, y;
+        lds_read2(lds_addr(st + L::kHi + i * 2048 + ((2 * kg) * 16 + lr) * 16),
+                  lds_addr(st + L::kHi + i * 2048 + ((2 * kg + 1) * 16 + lr) * 16), x, y);
+        al = cat(x, y);
+      } else if constexpr (kMode == kPrecise) {
+        const uint8_t* tl = st + (NP + i) * 4096;
+        v4i l0, l1, l2, l3;
+        lds_read4(lds_addr(tl + ((4 * kg + 0) * 16 + lr) * 16), lds_addr(tl + ((4 * kg + 1) * 16 + lr) * 16),
+                  lds_addr(tl + ((4 * kg + 2) * 16 + lr) * 16), lds_addr(tl + ((4 * kg + 3) * 16 + lr) * 16), l0, l1,
+                  l2, l3);
+        al16[0] = as_v8h(l0);
+        al16[1] = as_v8h(l1);
+        al16[2] = as_v8h(l2);
+        al16[3] = as_v8h(l3);
+      }
+#pragma unroll
+      for (int n = 0; n < 2; n++) {
+        v4f p = mfma_f16_block(ah, b16[n], v4f{0.f, 0.f, 0.f, 0.f});
+        if constexpr (kMode == kTwoTerms) p = mfma16x16x128_exp<127 - 11>(al, B[d][n], p);
+        if constexpr (kMode == kPrecise) p = mfma_f16_block(al16, b16[n], p);
+        acc[i][n][0] += p[0] * (sa.x * SW[d]);
+        acc[i][n][1] += p[1] * (sa.y * SW[d]);
+        acc[i][n][2] += p[2] * (sa.z * SW[d]);
+        acc[i][n][3] += p[3] * (sa.w * SW[d]);
+      }
+    }
+    issue(d, j + kLgDepth);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  __syncthreads();
+  // stage d's operations must all be issued before stage d + 1's: the per-step vmcnt wait
+  // counts operations in issue order
+#pragma unroll
+  for (int d = 0; d < kLgDepth; d++) {
+    issue(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  int j = 0;
+  for (; j + 2 * kLgDepth <= KB; j += 2 * kLgDepth) {
+#pragma unroll
+    for (int d = 0; d < 2 * kLgDepth; d++) step(d % kLgDepth, j + d);
+  }
+  for (; j < KB; j += kLgDepth) {
+#pragma unroll
+    for (int d = 0; d < kLgDepth; d++)
+      if (j + d < KB) step(d, j + d);
+  }
+  // no DMA may still target the ring when the next pass refills it or the workgroup ends
+  wait_vmcnt<0>();
+}
+
+// O rows of m-tiles [i0, i0 + NP), scaled by the routing weight.
+template <int NP>
+__device__ __forceinline__ void gemm2_large_store(const Plan& pl, float* __restrict__ obuf, int H, int row0, int rows,
+                                                  int hb, int i0, const v4f (&acc)[NP][2]) {
+  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < NP; i++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int row = 16 * (i0 + i) + 4 * kg + r;
+      if (row < rows) {
+        const int p = row0 + row;
+        const float w = pl.perm_w[p];
+#pragma unroll
+        for (int n = 0; n < 2; n++) obuf[(size_t)p * H + hb * kBlock + 32 * wave + 16 * n + lr] = acc[i][n][r] * w;
+      }
+    }
+  }
+}
+
+template <int MT>
+__global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, Plan pl, CHalf8 ch,
+                                                                     float* __restrict__ obuf) {
+  using L = G2L<MT>;
+  constexpr int NP = MT / 2;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
+  const int H = pb.H, HB = H / kBlock;
+  const int n_units = pl.info[5] * HB;
+  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const int mb = u / HB, hb = u - mb * HB;
+    const int4 blk = pl.mblocks2[mb];
+    const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), mt0 = uniform(blk.w);
+    const int mvalid = (rows + 15) / 16;
+    int any = 0;
+#pragma unroll
+    for (int i = 0; i < MT; i++) any |= i < mvalid ? pl.mt_flags[mt0 + i] : 0;
+    any = uniform(any);
+    if (any & kFlagExactProducts) {
+      // GEMM1 wrote this block's lo term in f16
+      for (int i0 = 0; i0 < mvalid; i0 += NP) {
+        v4f acc[NP][2];
+#pragma unroll
+        for (int i = 0; i < NP; i++) acc[i][0] = acc[i][1] = v4f{0.f, 0.f, 0.f, 0.f};
+        gemm2_large_pass<MT, NP, kPrecise>(pb, ch, ring, e, row0, rows, hb, i0, acc);
+        gemm2_large_store<NP>(pl, obuf, H, row0, rows, hb, i0, acc);
+      }
+    } else {
+      v4f acc[MT][2];
+#pragma unroll
+      for (int i = 0; i < MT; i++) acc[i][0] = acc[i][1] = v4f{0.f, 0.f, 0.f, 0.f};
+      if (any & kFlagTwoTermC) gemm2_large_pass<MT, MT, kTwoTerms>(pb, ch, ring, e, row0, rows, hb, 0, acc);
+      else gemm2_large_pass<MT, MT, kOneTerm>(pb, ch, ring, e, row0, rows, hb, 0, acc);
+      gemm2_large_store<MT>(pl, obuf, H, row0, rows, hb, 0, acc);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------ launch
+int large_grid() { return num_compute_units() * 2; }
+
+void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units,
+                        hipStream_t stream) {
+  const int grid = max_units < large_grid() ? max_units : large_grid();
+  if (grid <= 0) return;
+  switch (mt) {
+    case 2: hipLaunchKernelGGL(gemm1_large_kernel<2>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch); break;
+    default: hipLaunchKernelGGL(gemm1_large_kernel<4>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch); break;
+  }
+}
+
+void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
+                        hipStream_t stream) {
+  const int grid = max_units < large_grid() ? max_units : large_grid();
+  if (grid <= 0) return;
+  switch (mt) {
+    case 2: hipLaunchKernelGGL(gemm2_large_kernel<2>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, obuf); break;
+    default: hipLaunchKernelGGL(gemm2_large_kernel<4>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, obuf); break;
+  }
+}
+
+}  // namespace moefp8

@@ -19,16 +19,20 @@ namespace moefp8 {
 // Largest T served by the weight-streaming kernels.
 constexpr int64_t kDecodeMaxT = 64;
 
-int tile_m_for(int64_t T) {
-  if (T <= kDecodeMaxT) return 16;
-  return 64;
-}
+// m-tiles (16 rows) per GEMM m-block on the large-T path, from the expected rows per local
+// expert under uniform routing (T * 8 / 256 of them): 32-row blocks for a few dozen rows,
+// else 64 (larger blocks exceed the register file with 4 x 4 accumulator tiles per wave).
+int large_mt1(int64_t T) { return T / 32 >= 48 ? 4 : 2; }
+// GEMM2 must use GEMM1's m-blocks: GEMM1 picks a block's lo-term format, GEMM2 reads it
+int large_mt2(int64_t T) { return large_mt1(T); }
 
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
-  size_t tok_a2, esig, perm_exact, mtiles, c16, c16_scale, gbuf;
-  size_t cbuf, c_q, c_plane, c_scale, c_kmax, obuf, total;
-  int64_t pmax, max_mtiles, rows_cap;
+  size_t tok_a2, esig, perm_exact, mtiles, c16, c16_scale, gbuf, obuf;
+  size_t canon_token, bcnt, ccnt, mt_flags, mblocks1, mblocks2, c_hi, c_lo, c_lo16, c_scale;
+  size_t total;
+  int64_t pmax, max_mtiles, rows_cap, c_plane, max_mb1, max_mb2;
+  int nblk;
 };
 
 static size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -55,9 +59,8 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.tok_a2 = take((size_t)T * 4);
   L.esig = take((size_t)E_local * 2 * 4);
   L.perm_exact = take((size_t)pmax);
-  const int tm = tile_m_for(T);
-  L.max_mtiles = (pmax + tm - 1) / tm + E_local;
-  L.c_plane = align_up((size_t)pmax * I);
+  L.max_mtiles = (pmax + 15) / 16 + E_local;
+  L.c_plane = (int64_t)align_up((size_t)pmax * I);
   if (T <= kDecodeMaxT) {
     // small T: m-tile table, GEMM1 partials [rows][2I] fp32, C as f16 hi/lo planes + scales,
     // GEMM2 partials [rows][H] fp32; rows = pairs x K-split <= rows_cap
@@ -65,23 +68,28 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
     L.rows_cap = pmax > r8 ? pmax : r8;
     L.mtiles = take((size_t)L.max_mtiles * 16);
     L.gbuf = take((size_t)L.rows_cap * 2 * I * 4);
-    L.c16 = take(L.c_plane * 2 * 2);
+    L.c16 = take((size_t)L.c_plane * 2 * 2);
     L.c16_scale = take((size_t)pmax * (I / kBlock) * 4);
     L.obuf = take((size_t)L.rows_cap * H * 4);
     L.total = o;
     return L;
   }
-  // large T: kMaxTerms e4m3 planes of C [pmax, I] + fp32 scales [pmax, I/128] + per-sub-tile
-  // term counts, the f16 split of exact-product sub-tiles, and O [pmax][H] fp32
+  // large T: permutation scratch and tables, C (f16 hi, e4m3 or f16 lo, fp32 scales), O [pmax][H] fp32
   L.rows_cap = pmax;
-  const size_t c_scale_bytes = align_up((size_t)pmax * (I / kBlock) * 4);
-  const size_t c_kmax_bytes = (size_t)L.max_mtiles * (tm / 16) * (I / kBlock);
-  const size_t c_split = L.c_plane * kMaxTerms + c_scale_bytes + c_kmax_bytes;
-  L.cbuf = take(c_split);
-  L.c_q = L.cbuf;
-  L.c_scale = L.c_q + L.c_plane * kMaxTerms;
-  L.c_kmax = L.c_scale + c_scale_bytes;
-  L.c16 = take(L.c_plane * 2 * 2);
+  L.nblk = permute_large_blocks(T);
+  const int mt1 = large_mt1(T), mt2 = large_mt2(T);
+  L.max_mb1 = (pmax + 16 * mt1 - 1) / (16 * mt1) + E_local;
+  L.max_mb2 = (pmax + 16 * mt2 - 1) / (16 * mt2) + E_local;
+  L.canon_token = take((size_t)pmax * 4);
+  L.bcnt = take((size_t)L.nblk * E_local * 3 * 4);
+  L.ccnt = take((size_t)L.nblk * E_local * 4);
+  L.mt_flags = take((size_t)L.max_mtiles);
+  L.mblocks1 = take((size_t)L.max_mb1 * 16);
+  L.mblocks2 = take((size_t)L.max_mb2 * 16);
+  L.c_hi = take((size_t)pmax * I * 2);
+  L.c_lo = take((size_t)pmax * I);
+  L.c_lo16 = take((size_t)pmax * I * 2);
+  L.c_scale = take((size_t)pmax * (I / kBlock) * 4);
   L.obuf = take((size_t)pmax * H * 4);
   L.total = o;
   return L;
@@ -144,7 +152,7 @@ static int finish(const moefp8_args* a, const Layout& L, const int* topk_ids, co
   } copies[] = {{a->topk_ids, topk_ids, (size_t)T * kTopK * 4},
                 {a->topk_weights, topk_w, (size_t)T * kTopK * 4},
                 {a->expert_offsets, pl.expert_offsets, (size_t)(a->num_local_experts + 1) * 4},
-                {a->permuted_tokens, pl.perm_token, (size_t)L.pmax * 4}};
+                {a->permuted_tokens, pl.canon_token, (size_t)L.pmax * 4}};
   for (const Copy& c : copies)
     if (c.dst && hipMemcpyAsync(c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice, s) != hipSuccess)
       return MOEFP8_ERR_LAUNCH;
@@ -234,6 +242,10 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pl.info = reinterpret_cast<int*>(ws + L.info);
   pl.exact = ws + L.perm_exact;
   pl.mtiles = nullptr;
+  pl.mt_flags = nullptr;
+  pl.mblocks1 = nullptr;
+  pl.mblocks2 = nullptr;
+  pl.canon_token = pl.perm_token;
   float* tok_a2 = reinterpret_cast<float*>(ws + L.tok_a2);
   float* esig = reinterpret_cast<float*>(ws + L.esig);
 
@@ -249,7 +261,6 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pb.H = H;
   pb.I = I;
 
-  const int tile_m = tile_m_for(T);
   hipEvent_t* ev = reinterpret_cast<hipEvent_t*>(a->stage_events);
   auto mark = [&](int i) {
     if (ev) (void)hipEventRecord(ev[i], s);
@@ -287,27 +298,51 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
     mark(5);
     return finish(a, L, topk_ids, topk_w, pl, s);
   }
+  // large T: routing, permutation (3 launches), GEMM1 (+SwiGLU, C split), GEMM2, combine
+  LargePermArgs pa = {};
+  pa.topk_ids = topk_ids;
+  pa.topk_w = topk_w;
+  pa.tok_a2 = tok_a2;
+  pa.esig = esig;
+  pa.T = (int)T;
+  pa.E_local = E_local;
+  pa.offset = a->local_expert_offset;
+  pa.sqrt_i = sqrtf((float)I);
+  pa.nblk = L.nblk;
+  pa.bcnt = reinterpret_cast<int*>(ws + L.bcnt);
+  pa.ccnt = reinterpret_cast<int*>(ws + L.ccnt);
+  pa.expert_offsets = const_cast<int*>(pl.expert_offsets);
+  pa.mtile_offsets = const_cast<int*>(pl.mtile_offsets);
+  pa.active = const_cast<int*>(pl.active);
+  pa.info = const_cast<int*>(pl.info);
+  pa.perm_token = const_cast<int*>(pl.perm_token);
+  pa.perm_w = const_cast<float*>(pl.perm_w);
+  pa.canon_token = reinterpret_cast<int*>(ws + L.canon_token);
+  pa.tok_slot = const_cast<int*>(pl.tok_slot);
+  pa.mt_flags = ws + L.mt_flags;
+  pa.mblocks1 = reinterpret_cast<int4*>(ws + L.mblocks1);
+  pa.mblocks2 = reinterpret_cast<int4*>(ws + L.mblocks2);
+  pa.mt1 = large_mt1(T);
+  pa.mt2 = large_mt2(T);
+  pl.canon_token = pa.canon_token;
+  pl.mt_flags = pa.mt_flags;
+  pl.mblocks1 = pa.mblocks1;
+  pl.mblocks2 = pa.mblocks2;
+  CHalf8 ch;
+  ch.hi = reinterpret_cast<_Float16*>(ws + L.c_hi);
+  ch.lo = ws + L.c_lo;
+  ch.lo16 = reinterpret_cast<_Float16*>(ws + L.c_lo16);
+  ch.scale = reinterpret_cast<float*>(ws + L.c_scale);
+  float* obuf = reinterpret_cast<float*>(ws + L.obuf);
   mark(0);
   launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,
                topk_ids, topk_w, &mag, s);
   mark(1);
-  launch_permute(topk_ids, topk_w, (int)T, E_local, a->local_expert_offset, tile_m,
-                 const_cast<int*>(pl.expert_offsets), const_cast<int*>(pl.perm_token), const_cast<float*>(pl.perm_w),
-                 const_cast<int*>(pl.tok_slot), const_cast<int*>(pl.active), const_cast<int*>(pl.mtile_offsets),
-                 const_cast<int*>(pl.info), tok_a2, esig, I, const_cast<uint8_t*>(pl.exact), s);
+  launch_permute_large(pa, s);
   mark(2);
-  float* obuf = reinterpret_cast<float*>(ws + L.obuf);
-  {
-    CSplit cs;
-    cs.q = ws + L.c_q;
-    cs.plane = L.c_plane;
-    cs.scale = reinterpret_cast<float*>(ws + L.c_scale);
-    cs.kmax = ws + L.c_kmax;
-    cs.c16 = reinterpret_cast<_Float16*>(ws + L.c16);
-    launch_gemm1_prefill(pb, pl, tile_m, cs, (int)L.max_mtiles, s);
-    mark(3);
-    launch_gemm2_prefill(pb, pl, tile_m, cs, obuf, (int)L.max_mtiles, s);
-  }
+  launch_gemm1_large(pb, pl, ch, pa.mt1, (int)(L.max_mb1 * (I / kBlock)), s);
+  mark(3);
+  launch_gemm2_large(pb, pl, ch, obuf, pa.mt2, (int)(L.max_mb2 * (H / kBlock)), s);
   mark(4);
   launch_combine(pl, obuf, a->output, (int)T, H, s);
   mark(5);

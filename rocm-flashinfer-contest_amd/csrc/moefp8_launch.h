@@ -29,13 +29,6 @@ struct SplitPolicy {
 void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
                   int* topk_ids, float* topk_w, const MagInputs* mag, hipStream_t stream);
 
-// Stable counting sort of the local (token, expert) pairs (main.py:216-226), plus the
-// per-pair exact-product flag.
-void launch_permute(const int* topk_ids, const float* topk_w, int T, int E_local, int offset, int tile_m,
-                    int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
-                    int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
-                    uint8_t* perm_exact, hipStream_t stream);
-
 // The same permutation for T <= 64 in one workgroup with no serial loop, plus the
 // m-tile table (tile height 16) and the K-splits of the small-T GEMMs.
 void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset,
@@ -51,9 +44,13 @@ struct Plan {
   const int* tok_slot;        // [T * 8]
   const int* active;          // [E_local]
   const int* mtile_offsets;   // [E_local + 1]
-  const int* info;            // {P, n_active, m_tiles, S1, S2}: S1/S2 = K-splits of the small-T GEMMs
-  const uint8_t* exact;       // [Pmax] 1 = pair runs on the exact-product (f16 MFMA) path
-  const int4* mtiles;         // small T: per m-tile {expert, first pair, rows, 0}
+  const int* info;            // {P, n_active, m-blocks|m-tiles, S1, S2, GEMM2 m-blocks, m-tiles}
+  const uint8_t* exact;       // small T: [Pmax] per-pair flags (kFlagExactProducts, kFlagTwoTermC)
+  const int4* mtiles;         // small T: per m-tile {expert, first pair, rows, OR of pair flags}
+  const uint8_t* mt_flags;    // large T: per 16-row m-tile, OR of its pairs' flags
+  const int4* mblocks1;       // large T: GEMM1 m-blocks {expert, first row, rows, first m-tile}
+  const int4* mblocks2;       // large T: the same for GEMM2's m-block height
+  const int* canon_token;     // token of each pair in canonical (expert, token) order
 };
 
 struct Problem {
@@ -79,26 +76,47 @@ void launch_activation_decode(const Problem& pb, const Plan& pl, const float* gb
                               hipStream_t stream);
 void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, hipStream_t stream);
 
-// GEMM1 -> GEMM2 activations of the large-T path: up to kMaxTerms e4m3 planes of C,
-// one fp32 scale per (pair, 128 columns) and the term count of every 16-row sub-tile.
-struct CSplit {
-  uint8_t* q;       // [kMaxTerms][plane] bytes, plane = pmax * I
-  size_t plane;
-  float* scale;     // [pmax][I/128]
-  uint8_t* kmax;    // [max_mtiles][tile_m/16][I/128]: e4m3 term count, or kExactTerms
-  _Float16* c16;    // [2][pmax][I] two-term f16 split of C for exact-product sub-tiles
+// Large-T path (T > 64).  Permutation arguments: pair counts per (block of 256 tokens,
+// bucket = local expert x magnitude class) and the outputs of the three launches.
+struct LargePermArgs {
+  const int* topk_ids;
+  const float* topk_w;
+  const float* tok_a2;
+  const float* esig;
+  int T, E_local, offset;
+  float sqrt_i;
+  int nblk;
+  int* bcnt;            // [nblk][E_local * 3]
+  int* ccnt;            // [nblk][E_local]
+  int* expert_offsets;  // [E_local + 1]
+  int* mtile_offsets;   // [E_local + 1]
+  int* active;          // [E_local]
+  int* info;
+  int* perm_token;      // [Pmax] internal row order (class-grouped inside each expert)
+  float* perm_w;        // [Pmax]
+  int* canon_token;     // [Pmax] canonical order
+  int* tok_slot;        // [T * 8] internal rows of each token's pairs, ascending expert
+  uint8_t* mt_flags;    // [max m-tiles]
+  int4* mblocks1;       // GEMM1 m-blocks of mt1 m-tiles
+  int4* mblocks2;       // GEMM2 m-blocks of mt2 m-tiles
+  int mt1, mt2;
 };
+void launch_permute_large(const LargePermArgs& args, hipStream_t stream);
+int permute_large_blocks(int64_t T);
 
-// kmax marker of a sub-tile that runs GEMM2 on the exact-product path.
-constexpr int kExactTerms = 16;
+// C between the large-T GEMMs: hi = f16(C/s), lo = e4m3(2^11 (C/s - hi)), s per (pair, 128 cols).
+struct CHalf8 {
+  _Float16* hi;     // [Pmax][I]
+  uint8_t* lo;      // [Pmax][I], e4m3 lo term (m-blocks without exact-product pairs)
+  _Float16* lo16;   // [Pmax][I], f16 lo term (m-blocks with exact-product pairs)
+  float* scale;     // [Pmax][I/128]
+};
+int large_grid();
+void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units,
+                        hipStream_t stream);
+void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
+                        hipStream_t stream);
 
-// Large-T path: LDS-staged grouped GEMM1 (+SwiGLU + multi-term split of C) and GEMM2.
-void launch_gemm1_prefill(const Problem& pb, const Plan& pl, int tile_m, const CSplit& cs, int max_mtiles,
-                          hipStream_t stream);
-void launch_gemm2_prefill(const Problem& pb, const Plan& pl, int tile_m, const CSplit& cs, float* obuf,
-                          int max_mtiles, hipStream_t stream);
-
-// out[t] = bf16(sum over t's local pairs in ascending expert order of obuf[pair]) (main.py:240-243).
 void launch_combine(const Plan& pl, const float* obuf, uint16_t* out, int T, int H, hipStream_t stream);
 
 int num_compute_units();

@@ -1,0 +1,282 @@
+// Permutation of the (token, local expert) pairs for T > 64, in three launches over
+// blocks of 256 tokens (one token per thread):
+//
+//   count  per block, the number of pairs in each bucket (local expert, magnitude class)
+//   scan   one workgroup: bucket and expert offsets, the 16-row m-tile flags and the
+//          m-block tables of both grouped GEMMs
+//   place  per block, each pair's rank inside its bucket in token order gives its row;
+//          the rank inside its expert alone gives its canonical row
+//
+// Rows of an expert are grouped by magnitude class (class 0 first), each group in token
+// order, so pairs that need the exact-product or two-term paths share m-tiles instead of
+// spreading over all of them.  The canonical order -- for each local expert in
+// ascending order, its tokens ascending, as torch.nonzero yields them in
+// solutions/moe_fp8/main.py:216-226 -- is written separately (canon_token) for callers
+// that ask for the permutation.  Everything is a deterministic function of the routing.
+#include "moefp8_device.h"
+#include "moefp8_launch.h"
+
+namespace moefp8 {
+
+constexpr int kBlkTokens = 256;
+constexpr int kBlkWaves = kBlkTokens / kWave;
+constexpr int kClasses = 3;
+constexpr int kScanThreads = 1024;
+
+// 0: one f16 term of C is enough; 1: two terms; 2: two terms and exact GEMM1 products.
+__device__ __forceinline__ int magnitude_class(float pred) {
+  return pred > kPreciseRms ? 2 : (pred > kOneTermRms ? 1 : 0);
+}
+
+__device__ __forceinline__ uint8_t class_flags(int c) {
+  return c == 0 ? 0 : (c == 1 ? kFlagTwoTermC : (uint8_t)(kFlagTwoTermC | kFlagExactProducts));
+}
+
+// Bucket of slot k of token t, or -1 if the expert is not local.
+__device__ __forceinline__ int pair_bucket(const LargePermArgs& a, int t, int k, float a2, float* w_out, int* le_out) {
+  const int le = a.topk_ids[(size_t)t * kTopK + k] - a.offset;
+  if (le < 0 || le >= a.E_local) return -1;
+  const float w = a.topk_w[(size_t)t * kTopK + k];
+  const float pred = predicted_output_rms(a2, w, a.esig[2 * le], a.esig[2 * le + 1], a.sqrt_i);
+  *w_out = w;
+  *le_out = le;
+  return le * kClasses + magnitude_class(pred);
+}
+
+__global__ __launch_bounds__(kBlkTokens) void perm_count_kernel(LargePermArgs a) {
+  __shared__ int cnt[kEGlobal * kClasses];
+  const int E3 = a.E_local * kClasses, tid = threadIdx.x;
+  for (int i = tid; i < E3; i += kBlkTokens) cnt[i] = 0;
+  __syncthreads();
+  const int t = blockIdx.x * kBlkTokens + tid;
+  if (t < a.T) {
+    const float a2 = a.tok_a2[t];
+#pragma unroll
+    for (int k = 0; k < kTopK; k++) {
+      float w;
+      int le;
+      const int b = pair_bucket(a, t, k, a2, &w, &le);
+      if (b >= 0) atomicAdd(&cnt[b], 1);
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < E3; i += kBlkTokens) a.bcnt[(size_t)blockIdx.x * E3 + i] = cnt[i];
+}
+
+// First index i in [0, n) with v[i] > x (v ascending).
+__device__ __forceinline__ int upper_bound(const int* v, int n, int x) {
+  int lo = 0, hi = n;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (v[mid] <= x) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// Exclusive prefix sum over the wavefront (Hillis-Steele on shuffles).
+__device__ __forceinline__ int wave_exclusive_sum(int v) {
+  const int lane = lane_id();
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  return x - v;
+}
+
+__global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a) {
+  __shared__ int tot[kEGlobal * kClasses];
+  __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], emb1[kEGlobal + 1], emb2[kEGlobal + 1];
+  const int E = a.E_local, E3 = E * kClasses, nb = a.nblk, tid = threadIdx.x, lane = lane_id();
+
+  // canonical per-block base of each expert (relative), from the raw counts
+  for (int e = tid; e < E; e += kScanThreads) {
+    int run = 0;
+    for (int b = 0; b < nb; b++) {
+      const int* c = a.bcnt + (size_t)b * E3 + e * kClasses;
+      const int s = c[0] + c[1] + c[2];
+      a.ccnt[(size_t)b * E + e] = run;
+      run += s;
+    }
+  }
+  __syncthreads();
+  // per bucket: exclusive prefix over blocks (relative) and the total
+  for (int i = tid; i < E3; i += kScanThreads) {
+    int run = 0;
+    for (int b = 0; b < nb; b++) {
+      const int c = a.bcnt[(size_t)b * E3 + i];
+      a.bcnt[(size_t)b * E3 + i] = run;
+      run += c;
+    }
+    tot[i] = run;
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    int carry = 0, carry_mt = 0, carry_mb1 = 0, carry_mb2 = 0, carry_act = 0;
+    for (int e0 = 0; e0 < E; e0 += kWave) {
+      const int e = e0 + lane;
+      const int n = e < E ? tot[kClasses * e] + tot[kClasses * e + 1] + tot[kClasses * e + 2] : 0;
+      const int mt = (n + 15) / 16;
+      const int mb1 = (mt + a.mt1 - 1) / a.mt1, mb2 = (mt + a.mt2 - 1) / a.mt2;
+      const int pn = wave_exclusive_sum(n), pmt = wave_exclusive_sum(mt);
+      const int pmb1 = wave_exclusive_sum(mb1), pmb2 = wave_exclusive_sum(mb2);
+      const uint64_t act = __ballot(n > 0);
+      if (e < E) {
+        eoff[e] = carry + pn;
+        emt[e] = carry_mt + pmt;
+        emb1[e] = carry_mb1 + pmb1;
+        emb2[e] = carry_mb2 + pmb2;
+        a.expert_offsets[e] = carry + pn;
+        a.mtile_offsets[e] = carry_mt + pmt;
+        if (n > 0) a.active[carry_act + lanes_below(act)] = e;
+      }
+      carry += __builtin_amdgcn_readlane(pn + n, kWave - 1);
+      carry_mt += __builtin_amdgcn_readlane(pmt + mt, kWave - 1);
+      carry_mb1 += __builtin_amdgcn_readlane(pmb1 + mb1, kWave - 1);
+      carry_mb2 += __builtin_amdgcn_readlane(pmb2 + mb2, kWave - 1);
+      carry_act += (int)__popcll(act);
+    }
+    if (lane == 0) {
+      eoff[E] = carry;
+      emt[E] = carry_mt;
+      emb1[E] = carry_mb1;
+      emb2[E] = carry_mb2;
+      a.expert_offsets[E] = carry;
+      a.mtile_offsets[E] = carry_mt;
+      a.info[0] = carry;       // P
+      a.info[1] = carry_act;   // active experts
+      a.info[2] = carry_mb1;   // GEMM1 m-blocks
+      a.info[3] = 1;           // K-splits (small-T GEMMs only)
+      a.info[4] = 1;
+      a.info[5] = carry_mb2;   // GEMM2 m-blocks
+      a.info[6] = carry_mt;    // 16-row m-tiles
+    }
+  }
+  __syncthreads();
+  // absolute rows: bucket (e, c) starts after the expert's lower classes
+  for (int i = tid; i < nb * E3; i += kScanThreads) {
+    const int b3 = i % E3, e = b3 / kClasses, c = b3 - e * kClasses;
+    const int base = eoff[e] + (c > 0 ? tot[kClasses * e] : 0) + (c > 1 ? tot[kClasses * e + 1] : 0);
+    a.bcnt[i] += base;
+  }
+  for (int i = tid; i < nb * E; i += kScanThreads) a.ccnt[i] += eoff[i % E];
+  // m-tile flags: OR of the classes whose rows meet the tile
+  for (int g = tid; g < emt[E]; g += kScanThreads) {
+    const int e = upper_bound(emt, E + 1, g) - 1;
+    const int r0 = (g - emt[e]) * 16, r1 = r0 + 16;
+    const int n = eoff[e + 1] - eoff[e];
+    const int c1 = tot[kClasses * e], c2 = c1 + tot[kClasses * e + 1];
+    uint8_t f = 0;
+    if (r0 < c2 && r1 > c1) f |= class_flags(1);
+    if (r1 > c2 && r0 < n) f |= class_flags(2);
+    a.mt_flags[g] = f;
+  }
+  // m-block tables {expert, first row, rows, first m-tile}
+  for (int g = tid; g < emb1[E]; g += kScanThreads) {
+    const int e = upper_bound(emb1, E + 1, g) - 1, j = g - emb1[e];
+    const int n = eoff[e + 1] - eoff[e], r0 = j * 16 * a.mt1;
+    a.mblocks1[g] = int4{e, eoff[e] + r0, min(16 * a.mt1, n - r0), emt[e] + j * a.mt1};
+  }
+  for (int g = tid; g < emb2[E]; g += kScanThreads) {
+    const int e = upper_bound(emb2, E + 1, g) - 1, j = g - emb2[e];
+    const int n = eoff[e + 1] - eoff[e], r0 = j * 16 * a.mt2;
+    a.mblocks2[g] = int4{e, eoff[e] + r0, min(16 * a.mt2, n - r0), emt[e] + j * a.mt2};
+  }
+}
+
+// Rank of each slot's key among the lower lanes of the wavefront holding the same key
+// (keys of one lane are distinct or -1), plus the per-key count of the wavefront.  One
+// pass per distinct key present: ballots, no LDS atomics, deterministic.
+__device__ __forceinline__ void wave_key_ranks(const int (&key)[kTopK], int (&rank)[kTopK], int* counts) {
+  uint32_t todo = 0;
+#pragma unroll
+  for (int k = 0; k < kTopK; k++)
+    if (key[k] >= 0) todo |= 1u << k;
+  while (true) {
+    const uint64_t act = __ballot(todo != 0);
+    if (act == 0) break;
+    const int src = (int)__builtin_ctzll(act);
+    int mine = -1;
+#pragma unroll
+    for (int k = kTopK - 1; k >= 0; k--)
+      if ((todo >> k) & 1u) mine = key[k];
+    const int key0 = __builtin_amdgcn_readlane(mine, src);
+    uint64_t m = 0;
+    int slot = -1;
+#pragma unroll
+    for (int k = 0; k < kTopK; k++) {
+      const bool hit = key[k] == key0;
+      m |= __ballot(hit);
+      if (hit) slot = k;
+    }
+    const int r = lanes_below(m);
+#pragma unroll
+    for (int k = 0; k < kTopK; k++)
+      if (slot == k) {
+        rank[k] = r;
+        todo &= ~(1u << k);
+      }
+    if (lane_id() == src) counts[key0] = (int)__popcll(m);
+  }
+}
+
+__global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a) {
+  __shared__ int wcnt[kBlkWaves][kEGlobal * kClasses];
+  __shared__ int wcan[kBlkWaves][kEGlobal];
+  const int E = a.E_local, E3 = E * kClasses, tid = threadIdx.x, wave = tid >> 6;
+  for (int i = tid; i < kBlkWaves * kEGlobal * kClasses; i += kBlkTokens) (&wcnt[0][0])[i] = 0;
+  for (int i = tid; i < kBlkWaves * kEGlobal; i += kBlkTokens) (&wcan[0][0])[i] = 0;
+  __syncthreads();
+  const int t = blockIdx.x * kBlkTokens + tid;
+  const bool in = t < a.T;
+  int bk[kTopK], ek[kTopK], rb[kTopK], re[kTopK];
+  float wk[kTopK];
+  const float a2 = in ? a.tok_a2[t] : 0.f;
+#pragma unroll
+  for (int k = 0; k < kTopK; k++) {
+    bk[k] = -1;
+    ek[k] = -1;
+    wk[k] = 0.f;
+    rb[k] = 0;
+    re[k] = 0;
+    if (in) {
+      int le = -1;
+      bk[k] = pair_bucket(a, t, k, a2, &wk[k], &le);
+      ek[k] = bk[k] >= 0 ? le : -1;
+    }
+  }
+  wave_key_ranks(bk, rb, wcnt[wave]);
+  wave_key_ranks(ek, re, wcan[wave]);
+  __syncthreads();
+  if (!in) return;
+  int kk = 0;
+#pragma unroll
+  for (int k = 0; k < kTopK; k++) {
+    if (bk[k] < 0) continue;
+    int pos = a.bcnt[(size_t)blockIdx.x * E3 + bk[k]] + rb[k];
+    int cpos = a.ccnt[(size_t)blockIdx.x * E + ek[k]] + re[k];
+    for (int w = 0; w < wave; w++) {
+      pos += wcnt[w][bk[k]];
+      cpos += wcan[w][ek[k]];
+    }
+    a.perm_token[pos] = t;
+    a.perm_w[pos] = wk[k];
+    a.canon_token[cpos] = t;
+    a.tok_slot[(size_t)t * kTopK + kk] = pos;
+    kk++;
+  }
+  for (; kk < kTopK; kk++) a.tok_slot[(size_t)t * kTopK + kk] = -1;
+}
+
+void launch_permute_large(const LargePermArgs& args, hipStream_t stream) {
+  if (args.nblk <= 0) return;
+  hipLaunchKernelGGL(perm_count_kernel, dim3(args.nblk), dim3(kBlkTokens), 0, stream, args);
+  hipLaunchKernelGGL(perm_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, args);
+  hipLaunchKernelGGL(perm_place_kernel, dim3(args.nblk), dim3(kBlkTokens), 0, stream, args);
+}
+
+int permute_large_blocks(int64_t T) { return (int)((T + kBlkTokens - 1) / kBlkTokens); }
+
+}  // namespace moefp8

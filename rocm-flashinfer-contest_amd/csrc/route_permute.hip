@@ -5,9 +5,10 @@
 //                canonical arithmetic of the oracle: fp64-evaluated sigmoid rounded
 //                once to fp32, (value desc, index asc) ranking for groups and
 //                experts, ascending-id output, sequential fp32 normaliser.
-// permute_kernel restates the selection of main.py:216-226: for each local
-//                expert in ascending order, the tokens that picked it in ascending
-//                token order (torch.nonzero), as one stable counting sort.
+// permute_small_kernel restates the selection of main.py:216-226 for T <= 64: for
+//                each local expert in ascending order, the tokens that picked it in
+//                ascending token order (torch.nonzero), as one stable counting sort
+//                (larger T: permute_large.hip).
 #include "moefp8_device.h"
 #include "moefp8_launch.h"
 
@@ -267,118 +268,6 @@ __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __rest
   }
 }
 
-// Single-workgroup stable counting sort of (token, local expert) pairs.
-//   counts/offsets  per local expert (main.py:222, 225)
-//   perm_token[p]   token of pair p, expert-major, token-ascending
-//   perm_w[p]       routing weight of pair p (main.py:240)
-//   tok_slot[t][k]  pair index of token t's k-th local expert (ascending expert), -1 padded
-//   active[]        local experts with >= 1 token, ascending; info[] totals
-constexpr int kPermThreads = 1024;
-constexpr int kPermWaves = kPermThreads / kWave;
-
-__global__ __launch_bounds__(kPermThreads) void permute_kernel(
-    const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int E_local, int offset,
-    int tile_m, int* __restrict__ expert_offsets, int* __restrict__ perm_token, float* __restrict__ perm_w,
-    int* __restrict__ tok_slot, int* __restrict__ active, int* __restrict__ mtile_offsets,
-    int* __restrict__ info, const float* __restrict__ tok_a2, const float* __restrict__ esig, float sqrt_i,
-    uint8_t* __restrict__ perm_exact) {
-  __shared__ int cnt[kEGlobal];
-  __shared__ int base[kEGlobal];
-  __shared__ int wcnt[kPermWaves][kEGlobal];
-  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-
-  for (int e = tid; e < E_local; e += kPermThreads) cnt[e] = 0;
-  __syncthreads();
-  for (int i = tid; i < T * kTopK; i += kPermThreads) {
-    const int le = topk_ids[i] - offset;
-    if (le >= 0 && le < E_local) atomicAdd(&cnt[le], 1);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0, n_act = 0, mt = 0;
-    for (int e = 0; e < E_local; e++) {
-      expert_offsets[e] = run;
-      mtile_offsets[e] = mt;
-      base[e] = run;
-      run += cnt[e];
-      mt += (cnt[e] + tile_m - 1) / tile_m;
-      if (cnt[e] > 0) active[n_act++] = e;
-    }
-    expert_offsets[E_local] = run;
-    mtile_offsets[E_local] = mt;
-    info[0] = run;    // P
-    info[1] = n_act;  // active experts
-    info[2] = mt;     // m-tiles of height tile_m
-    info[3] = 1;      // K-splits (small-T GEMMs only)
-    info[4] = 1;
-  }
-  __syncthreads();
-
-  for (int c0 = 0; c0 < T; c0 += kPermThreads) {
-    const int t = c0 + tid;
-    int les[kTopK], slots[kTopK], rank[kTopK];
-    int n = 0;
-    if (t < T) {
-#pragma unroll
-      for (int j = 0; j < kTopK; j++) {
-        const int le = topk_ids[t * kTopK + j] - offset;
-        if (le >= 0 && le < E_local) {
-#pragma unroll
-          for (int k = 0; k < kTopK; k++)
-            if (k == n) {
-              les[k] = le;
-              slots[k] = j;
-            }
-          n++;
-        }
-      }
-    }
-    int ptr = 0;
-    for (int e = 0; e < E_local; e++) {
-      int cur = -1;
-#pragma unroll
-      for (int k = 0; k < kTopK; k++)
-        if (k == ptr) cur = les[k];
-      const bool pick = ptr < n && cur == e;
-      const uint64_t m = __ballot(pick);
-      if (lane == 0) wcnt[wave][e] = __popcll(m);
-      if (pick) {
-        const int r = __popcll(m & ((1ull << lane) - 1ull));
-#pragma unroll
-        for (int k = 0; k < kTopK; k++)
-          if (k == ptr) rank[k] = r;
-        ptr++;
-      }
-    }
-    __syncthreads();
-    for (int e = tid; e < E_local; e += kPermThreads) {
-      int run = base[e];
-      for (int w = 0; w < kPermWaves; w++) {
-        const int c = wcnt[w][e];
-        wcnt[w][e] = run;
-        run += c;
-      }
-      base[e] = run;
-    }
-    __syncthreads();
-    if (t < T) {
-#pragma unroll
-      for (int k = 0; k < kTopK; k++) {
-        int pos = -1;
-        if (k < n) {
-          pos = wcnt[wave][les[k]] + rank[k];
-          const float w = topk_w[t * kTopK + slots[k]];
-          perm_token[pos] = t;
-          perm_w[pos] = w;
-          perm_exact[pos] = needs_exact_products(tok_a2[t], w, esig[2 * les[k]], esig[2 * les[k] + 1], sqrt_i);
-        }
-        tok_slot[t * kTopK + k] = pos;
-      }
-    }
-    __syncthreads();
-  }
-}
-
 // Largest K-split S in {8, 4, 2, 1} whose units still fit the grid and the partial rows.
 __device__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap) {
   for (int S = 8; S > 1; S >>= 1)
@@ -516,13 +405,5 @@ void launch_route(const void* logits, int logits_dt, const void* bias, int bias_
                      bias, bias_dt, T, rsf, topk_ids, topk_w, (int)blocks, mg);
 }
 
-void launch_permute(const int* topk_ids, const float* topk_w, int T, int E_local, int offset, int tile_m,
-                    int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
-                    int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
-                    uint8_t* perm_exact, hipStream_t stream) {
-  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPermThreads), 0, stream, topk_ids, topk_w, T, E_local,
-                     offset, tile_m, expert_offsets, perm_token, perm_w, tok_slot, active, mtile_offsets, info,
-                     tok_a2, esig, sqrtf((float)I), perm_exact);
-}
 
 }  // namespace moefp8
