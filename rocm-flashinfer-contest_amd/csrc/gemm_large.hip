@@ -94,6 +94,34 @@ __device__ __forceinline__ void lds_read5(uint32_t a0, uint32_t a1, uint32_t a2,
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
 
+// DMA and its completion wait as inline asm, for kernels whose LDS operand reads are ordinary
+// loads: the compiler then neither knows of the DMAs nor drains them before every LDS read, and
+// schedules the reads with exact lgkmcnt waits.  The writer of M0 must precede the DMA by one
+// wait state.
+__device__ __forceinline__ void dma_lds16(const void* g, uint32_t lds_uniform) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds_uniform)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma_lds4(const void* g, uint32_t lds_uniform) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(lds_uniform)
+               : "memory", "m0");
+}
+// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset.
+__device__ __forceinline__ void dma_lds16_s(uint32_t voff, const void* sbase, uint32_t lds_uniform) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase),
+               "s"(lds_uniform) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_lds4_s(uint32_t voff, const void* sbase, uint32_t lds_uniform) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase),
+               "s"(lds_uniform) : "memory", "m0");
+}
+// s_barrier, then no memory access may move above it
+__device__ __forceinline__ void barrier_lds() {
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+#define MOEFP8_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+
 // Wave-uniform read of kernel-constant data through the constant address space, so the
 // compiler can use a scalar load (counted by lgkmcnt, not by the vmcnt pipeline above).
 __device__ __forceinline__ float load_uniform(const float* p) {
@@ -306,34 +334,222 @@ __device__ __forceinline__ void gemm1_large_store(const Plan& pl, const CHalf8& 
   __syncthreads();
 }
 
+// Units (m-block, 128 output columns) over blocks [first, info[2]) of the table; first = 0, or
+// info[7] (the exact-product blocks after the class 0/1 blocks that the 128-row kernel takes).
 template <int MT>
-__global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, Plan pl, CHalf8 ch) {
+__global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, Plan pl, CHalf8 ch, int from_exact) {
   using L = G1L<MT>;
   static_assert(MT % 2 == 0, "two activation DMAs per m-tile");
   __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
   __shared__ float amax_s[kLgWaves][16 * MT];
   const int I = pb.I, NCB = I / kBlock;
-  const int n_units = pl.info[2] * NCB;
+  const int mb_first = from_exact ? pl.info[7] : 0;
+  const int n_units = (pl.info[2] - mb_first) * NCB;
 
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-    const int mb = u / NCB, cb = u - mb * NCB;
-    const int4 blk = pl.mblocks1[mb];
-    const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), mt0 = uniform(blk.w);
+    const int mb = mb_first + u / NCB, cb = u % NCB;
+    const int4 blk = pl.mblocks[mb];
+    const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
     const int mvalid = (rows + 15) / 16;
-    int any_exact = 0;
-#pragma unroll
-    for (int i = 0; i < MT; i++) any_exact |= i < mvalid ? pl.mt_flags[mt0 + i] & kFlagExactProducts : 0;
-    if (!uniform(any_exact)) {
+    if (!(flags & kFlagExactProducts)) {
       v4f acc[MT][4];
       gemm1_large_pass<MT, MT, false>(pb, pl, ring, e, row0, rows, cb, 0, acc);
       gemm1_large_store<MT, MT, false>(pl, ch, amax_s, I, row0, rows, cb, 0, acc);
     } else {
-      // rare: two m-tiles per pass over K, with exact products (the f16 MFMA on widened
-      // operands needs the registers of the fp8 path twice over)
+      // two m-tiles per pass over K, with exact products (the f16 MFMA on widened operands
+      // needs the registers of the fp8 path twice over)
       for (int i0 = 0; i0 < mvalid; i0 += 2) {
         v4f acc[2][4];
         gemm1_large_pass<MT, 2, true>(pb, pl, ring, e, row0, rows, cb, i0, acc);
         gemm1_large_store<MT, 2, true>(pl, ch, amax_s, I, row0, rows, cb, i0, acc);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------ GEMM1, 128-row m-blocks
+// For the 128-row blocks over an expert's class 0 and 1 rows.  A workgroup of 8 wavefronts (one
+// per CU, two per SIMD, 148 KB of LDS) owns one unit = (m-block, 128 C columns = 256 weight rows,
+// 128 up and 128 gate) and stages BOTH operands of each K-block through a 3-stage LDS ring by
+// DMA: the weight rows are read once per unit and shared by the block's 128 rows (the
+// per-wavefront weight streams above re-read them per 64 rows through the vector-memory path).
+// Wavefront w = (wm, wn) = (w % 2, w / 2) computes rows 64 wm .. 64 wm + 63 x its 64 weight rows
+// (C columns 32 wn .. 32 wn + 31, up and gate): 4 x 4 MFMA 16x16x128 tiles per K-block, 64
+// accumulator registers, so that the two wavefronts of a SIMD hide each other's MFMA and LDS
+// latencies.
+//
+// The DMAs and their wait are inline asm and the LDS operand reads ordinary loads: the compiler
+// schedules the reads with exact lgkmcnt waits and never drains the DMAs before them.
+//
+// LDS stage: A [128 rows][128 B], B [256 rows][128 B], 128 row scales.  A row's 16-byte chunk c
+// sits in slot c ^ key(row), key(row) = (row & 7) ^ ((row >> 3) & 1): a DMA instruction writes 8
+// rows x 8 slots in lane order (each lane fetching the chunk that belongs in its slot, 8 lanes
+// per 128-byte row segment), and an MFMA operand read (16 rows, two chunks per lane) puts any 16
+// consecutive lanes on distinct 16-byte bank groups of a 256-byte bank row (and any 8 on distinct
+// ones of a 128-byte row).
+constexpr int kBgWaves = 8;
+constexpr int kBgThreads = 64 * kBgWaves;
+constexpr int kBgRows = 128;
+constexpr int kBgWRows = 256;
+constexpr int kBgStages = 3;
+constexpr int kBgA = kBgRows * 128;
+constexpr int kBgB = kBgWRows * 128;
+constexpr int kBgStage = kBgA + kBgB + kBgRows * 4;
+constexpr int kBgOps = 2 + 4 + 1;            // per wavefront and K-block: A, B and row-scale DMAs
+
+__device__ __forceinline__ int bg_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+__global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Plan pl, CHalf8 ch) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kBgStages * kBgStage];
+  __shared__ __attribute__((aligned(16))) float2 sw_s[kBigMaxKB];
+  __shared__ float amax_s[4][kBgRows];
+  const int H = pb.H, I = pb.I, T = pb.T, KB = H / kBlock, NCB = I / kBlock;
+  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+  const int n_units = pl.info[7] * NCB;
+  // DMA lane roles: row (lane / 8) of an 8-row group, slot lane % 8
+  const int drow = lane >> 3, dslot = lane & 7;
+  // operand read offsets inside a 16-row tile (swizzled chunks 2kg and 2kg + 1 of row lr)
+  const int rd0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
+  const int rd1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
+  const uint32_t ring_lds = uniform((int)lds_addr(ring));
+
+  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const int mb = u / NCB, cb = u % NCB;
+    const int4 blk = pl.mblocks[mb];
+    const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
+    // DMA sources as per-lane byte offsets from wave-uniform bases: A rows 16w + 8q + drow (the
+    // tokens' hidden rows), B LDS rows 32w + 8q + drow (LDS row R holds n-tile (R % 64) / 16 of
+    // weight-row group R / 64: 0, 1 up, 2, 3 gate), row scales of rows 64 (w % 2) + lane
+    uint32_t aoff[2], boff[4];
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+      const int r = 16 * wave + 8 * q + drow;
+      const int tok = pl.perm_token[row0 + min(r, rows - 1)];
+      aoff[q] = (uint32_t)tok * (uint32_t)H + (uint32_t)((dslot ^ bg_key(r)) * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int R = 32 * wave + 8 * q + drow;
+      const int g = R >> 6, n = (R >> 4) & 3, rr = R & 15;
+      const int wrow = (n < 2 ? 0 : I) + cb * kBlock + 32 * g + 16 * (n & 1) + rr;
+      boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ bg_key(R)) * 16);
+    }
+    const uint32_t soff = 4u * (uint32_t)pl.perm_token[row0 + min(64 * (wave & 1) + lane, rows - 1)];
+    const uint8_t* wbase = pb.w13 + (size_t)e * 2 * I * H;
+    auto issue = [&](int j) {
+      const int k = min(j, KB - 1);
+      const uint32_t st = ring_lds + (uint32_t)((j % kBgStages) * kBgStage);
+      const uint8_t* abase = pb.hidden + (size_t)k * kBlock;
+      const uint8_t* bbase = wbase + (size_t)k * kBlock;
+      const float* sbase = pb.hscale + (size_t)k * T;
+#pragma unroll
+      for (int q = 0; q < 2; q++) dma_lds16_s(aoff[q], abase, st + (16 * wave + 8 * q) * 128);
+#pragma unroll
+      for (int q = 0; q < 4; q++) dma_lds16_s(boff[q], bbase, st + kBgA + (32 * wave + 8 * q) * 128);
+      // wavefronts 2..7 repeat the row scales of 0 and 1 (same bytes), so that every wavefront
+      // issues the same operations
+      dma_lds4_s(soff, sbase, st + kBgA + kBgB + (wave & 1) * 256);
+    };
+
+    // the previous unit's readers are done with the ring, amax_s and sw_s
+    __syncthreads();
+    // weight scales of the unit: {up, gate} per K-block
+    {
+      const float* su = pb.s13 + ((size_t)e * (2 * I / kBlock) + cb) * KB;
+      const float* sg = su + (size_t)NCB * KB;
+      const int t = threadIdx.x;
+      if (t < KB) sw_s[t] = float2{su[t], sg[t]};
+    }
+    __syncthreads();
+    // the table and scale loads above are complete: only DMAs count from here
+    MOEFP8_WAIT_VMCNT(0);
+    for (int d = 0; d < kBgStages - 1; d++) issue(d);
+    v4f acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    for (int j = 0; j < KB; j++) {
+      // stage j's DMAs are done once only the following stage's (7 per wavefront) may be in flight
+      static_assert((kBgStages - 2) * kBgOps == 7, "wait count");
+      MOEFP8_WAIT_VMCNT(7);
+      barrier_lds();
+      const uint8_t* st = ring + (j % kBgStages) * kBgStage;
+      v8i B[4];
+#pragma unroll
+      for (int n = 0; n < 4; n++) {
+        const uint8_t* bt = st + kBgA + (64 * wn + 16 * n) * 128;
+        B[n] = cat(*reinterpret_cast<const v4i*>(bt + rd0), *reinterpret_cast<const v4i*>(bt + rd1));
+      }
+      const float2 sw = sw_s[j];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int t = 4 * wm + i;
+        const uint8_t* at = st + t * 16 * 128;
+        const v8i a = cat(*reinterpret_cast<const v4i*>(at + rd0), *reinterpret_cast<const v4i*>(at + rd1));
+        const float4 sa = *reinterpret_cast<const float4*>(st + kBgA + kBgB + (16 * t + 4 * kg) * 4);
+        const float4 su = {sa.x * sw.x, sa.y * sw.x, sa.z * sw.x, sa.w * sw.x};
+        const float4 sg = {sa.x * sw.y, sa.y * sw.y, sa.z * sw.y, sa.w * sw.y};
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+          const float4 sc = n < 2 ? su : sg;
+          const v4f p = mfma16x16x128(a, B[n], v4f{0.f, 0.f, 0.f, 0.f});
+          acc[i][n][0] += p[0] * sc.x;
+          acc[i][n][1] += p[1] * sc.y;
+          acc[i][n][2] += p[2] * sc.z;
+          acc[i][n][3] += p[3] * sc.w;
+        }
+      }
+      // stage (j + 2) % 3 was last read at step j - 1, before this step's barrier
+      issue(j + kBgStages - 1);
+    }
+    MOEFP8_WAIT_VMCNT(0);
+
+    // epilogue: C = silu(gate) * up, per-row max over the unit's 128 columns, hi/lo split
+    const int col0 = cb * kBlock + 32 * wn;
+    float c[4][2][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int jn = 0; jn < 2; jn++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) c[i][jn][r] = silu_f32(acc[i][jn + 2][r]) * acc[i][jn][r];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float m = fmaxf(fabsf(c[i][0][r]), fabsf(c[i][1][r]));
+        m = fmaxf(m, dpp_f32<kDppXor1>(m));
+        m = fmaxf(m, dpp_f32<kDppXor2>(m));
+        m = fmaxf(m, dpp_f32<kDppHalfMirror>(m));
+        m = fmaxf(m, dpp_f32<kDppRowMirror>(m));
+        if (lr == 0) amax_s[wn][16 * (4 * wm + i) + 4 * kg + r] = m;
+      }
+    }
+    __syncthreads();
+    const bool two = (flags & kFlagTwoTermC) != 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int row = 16 * (4 * wm + i) + 4 * kg + r;
+        if (row >= rows) continue;
+        const float amax = fmaxf(fmaxf(amax_s[0][row], amax_s[1][row]), fmaxf(amax_s[2][row], amax_s[3][row]));
+        float inv, scale;
+        split_scale(amax, inv, scale);
+        const size_t p = (size_t)(row0 + row);
+#pragma unroll
+        for (int jn = 0; jn < 2; jn++) {
+          const int col = col0 + 16 * jn + lr;
+          const float v = fminf(fmaxf(c[i][jn][r] * inv, -448.0f), 448.0f);
+          const _Float16 hi = (_Float16)v;
+          ch.hi[p * I + col] = hi;
+          if (two)
+            ch.lo[p * I + col] = (uint8_t)f32_to_e4m3(fminf(fmaxf((v - (float)hi) * kLoScale, -448.0f), 448.0f));
+        }
+        if (wn == 0 && lr == 0) ch.scale[p * NCB + cb] = scale;
       }
     }
   }
@@ -512,6 +728,8 @@ __device__ __forceinline__ void gemm2_large_store(const Plan& pl, float* __restr
   }
 }
 
+// Units (m-block, 128 output columns) over the whole block table; a block taller than 16 MT
+// rows (the 128-row class 0/1 blocks) is taken 16 MT rows at a time.
 template <int MT>
 __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, Plan pl, CHalf8 ch,
                                                                      float* __restrict__ obuf) {
@@ -522,29 +740,28 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
   const int n_units = pl.info[5] * HB;
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
     const int mb = u / HB, hb = u - mb * HB;
-    const int4 blk = pl.mblocks2[mb];
-    const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), mt0 = uniform(blk.w);
-    const int mvalid = (rows + 15) / 16;
-    int any = 0;
+    const int4 blk = pl.mblocks[mb];
+    const int e = uniform(blk.x), flags = uniform(blk.w);
+    for (int s0 = 0; s0 < blk.z; s0 += 16 * MT) {
+      const int row0 = uniform(blk.y + s0), rows = uniform(min(16 * MT, blk.z - s0));
+      const int mvalid = (rows + 15) / 16;
+      if (flags & kFlagExactProducts) {
+        // GEMM1 wrote this block's lo term in f16
+        for (int i0 = 0; i0 < mvalid; i0 += NP) {
+          v4f acc[NP][2];
 #pragma unroll
-    for (int i = 0; i < MT; i++) any |= i < mvalid ? pl.mt_flags[mt0 + i] : 0;
-    any = uniform(any);
-    if (any & kFlagExactProducts) {
-      // GEMM1 wrote this block's lo term in f16
-      for (int i0 = 0; i0 < mvalid; i0 += NP) {
-        v4f acc[NP][2];
+          for (int i = 0; i < NP; i++) acc[i][0] = acc[i][1] = v4f{0.f, 0.f, 0.f, 0.f};
+          gemm2_large_pass<MT, NP, kPrecise>(pb, ch, ring, e, row0, rows, hb, i0, acc);
+          gemm2_large_store<NP>(pl, obuf, H, row0, rows, hb, i0, acc);
+        }
+      } else {
+        v4f acc[MT][2];
 #pragma unroll
-        for (int i = 0; i < NP; i++) acc[i][0] = acc[i][1] = v4f{0.f, 0.f, 0.f, 0.f};
-        gemm2_large_pass<MT, NP, kPrecise>(pb, ch, ring, e, row0, rows, hb, i0, acc);
-        gemm2_large_store<NP>(pl, obuf, H, row0, rows, hb, i0, acc);
+        for (int i = 0; i < MT; i++) acc[i][0] = acc[i][1] = v4f{0.f, 0.f, 0.f, 0.f};
+        if (flags & kFlagTwoTermC) gemm2_large_pass<MT, MT, kTwoTerms>(pb, ch, ring, e, row0, rows, hb, 0, acc);
+        else gemm2_large_pass<MT, MT, kOneTerm>(pb, ch, ring, e, row0, rows, hb, 0, acc);
+        gemm2_large_store<MT>(pl, obuf, H, row0, rows, hb, 0, acc);
       }
-    } else {
-      v4f acc[MT][2];
-#pragma unroll
-      for (int i = 0; i < MT; i++) acc[i][0] = acc[i][1] = v4f{0.f, 0.f, 0.f, 0.f};
-      if (any & kFlagTwoTermC) gemm2_large_pass<MT, MT, kTwoTerms>(pb, ch, ring, e, row0, rows, hb, 0, acc);
-      else gemm2_large_pass<MT, MT, kOneTerm>(pb, ch, ring, e, row0, rows, hb, 0, acc);
-      gemm2_large_store<MT>(pl, obuf, H, row0, rows, hb, 0, acc);
     }
   }
 }
@@ -552,14 +769,26 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
 // ------------------------------------------------------------------------------------------ launch
 int large_grid() { return num_compute_units() * 2; }
 
-void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units,
+void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units, int from_exact,
                         hipStream_t stream) {
   const int grid = max_units < large_grid() ? max_units : large_grid();
   if (grid <= 0) return;
   switch (mt) {
-    case 2: hipLaunchKernelGGL(gemm1_large_kernel<2>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch); break;
-    default: hipLaunchKernelGGL(gemm1_large_kernel<4>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch); break;
+    case 2:
+      hipLaunchKernelGGL(gemm1_large_kernel<2>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, from_exact);
+      break;
+    default:
+      hipLaunchKernelGGL(gemm1_large_kernel<4>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, from_exact);
+      break;
   }
+}
+
+void launch_gemm1_big(const Problem& pb, const Plan& pl, const CHalf8& ch, int max_units, hipStream_t stream) {
+  static_assert(kBigRows == kBgRows, "block height");
+  const int cus = num_compute_units();
+  const int grid = max_units < cus ? max_units : cus;
+  if (grid <= 0) return;
+  hipLaunchKernelGGL(gemm1_big_kernel, dim3(grid), dim3(kBgThreads), 0, stream, pb, pl, ch);
 }
 
 void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,

@@ -19,19 +19,24 @@ namespace moefp8 {
 // Largest T served by the weight-streaming kernels.
 constexpr int64_t kDecodeMaxT = 64;
 
-// m-tiles (16 rows) per GEMM m-block on the large-T path, from the expected rows per local
-// expert under uniform routing (T * 8 / 256 of them): 32-row blocks for a few dozen rows,
-// else 64 (larger blocks exceed the register file with 4 x 4 accumulator tiles per wave).
-int large_mt1(int64_t T) { return T / 32 >= 48 ? 4 : 2; }
-// GEMM2 must use GEMM1's m-blocks: GEMM1 picks a block's lo-term format, GEMM2 reads it
-int large_mt2(int64_t T) { return large_mt1(T); }
+// Large-T m-blocks, from the expected rows per local expert under uniform routing (T * 8 / 256
+// of them).  From T = 2048 (64 rows per expert) the class 0/1 rows of an expert go in 128-row
+// blocks for the LDS-staged GEMM1 and its exact-product rows in 32-row blocks; below, all rows
+// go in blocks of 16 * large_mt(T) rows (32 for a few dozen rows per expert, else 64).
+constexpr int64_t kBigT = 2048;
+constexpr int kExactRows = 32;
+// (the 128-row GEMM1 addresses hidden rows with 32-bit byte offsets)
+bool large_big(int64_t T, int H) { return T >= kBigT && H / kBlock <= kBigMaxKB && T * H < ((int64_t)1 << 31); }
+int large_mt(int64_t T) { return T / 32 >= 48 ? 4 : 2; }
+int large_rows_a(int64_t T, int H) { return large_big(T, H) ? kBigRows : 16 * large_mt(T); }
+int large_rows_b(int64_t T, int H) { return large_big(T, H) ? kExactRows : 16 * large_mt(T); }
 
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
   size_t tok_a2, esig, perm_exact, mtiles, c16, c16_scale, gbuf, obuf;
-  size_t canon_token, bcnt, ccnt, mt_flags, mblocks1, mblocks2, c_hi, c_lo, c_lo16, c_scale;
+  size_t canon_token, bcnt, ccnt, mblocks, c_hi, c_lo, c_lo16, c_scale;
   size_t total;
-  int64_t pmax, max_mtiles, rows_cap, c_plane, max_mb1, max_mb2;
+  int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks_a, max_blocks;
   int nblk;
 };
 
@@ -77,15 +82,13 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   // large T: permutation scratch and tables, C (f16 hi, e4m3 or f16 lo, fp32 scales), O [pmax][H] fp32
   L.rows_cap = pmax;
   L.nblk = permute_large_blocks(T);
-  const int mt1 = large_mt1(T), mt2 = large_mt2(T);
-  L.max_mb1 = (pmax + 16 * mt1 - 1) / (16 * mt1) + E_local;
-  L.max_mb2 = (pmax + 16 * mt2 - 1) / (16 * mt2) + E_local;
+  const int ra = large_rows_a(T, H), rb = large_rows_b(T, H);
+  L.max_blocks_a = (pmax + ra - 1) / ra + E_local;
+  L.max_blocks = L.max_blocks_a + (pmax + rb - 1) / rb + E_local;
   L.canon_token = take((size_t)pmax * 4);
   L.bcnt = take((size_t)L.nblk * E_local * 3 * 4);
   L.ccnt = take((size_t)L.nblk * E_local * 4);
-  L.mt_flags = take((size_t)L.max_mtiles);
-  L.mblocks1 = take((size_t)L.max_mb1 * 16);
-  L.mblocks2 = take((size_t)L.max_mb2 * 16);
+  L.mblocks = take((size_t)L.max_blocks * 16);
   L.c_hi = take((size_t)pmax * I * 2);
   L.c_lo = take((size_t)pmax * I);
   L.c_lo16 = take((size_t)pmax * I * 2);
@@ -242,9 +245,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pl.info = reinterpret_cast<int*>(ws + L.info);
   pl.exact = ws + L.perm_exact;
   pl.mtiles = nullptr;
-  pl.mt_flags = nullptr;
-  pl.mblocks1 = nullptr;
-  pl.mblocks2 = nullptr;
+  pl.mblocks = nullptr;
   pl.canon_token = pl.perm_token;
   float* tok_a2 = reinterpret_cast<float*>(ws + L.tok_a2);
   float* esig = reinterpret_cast<float*>(ws + L.esig);
@@ -319,15 +320,11 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pa.perm_w = const_cast<float*>(pl.perm_w);
   pa.canon_token = reinterpret_cast<int*>(ws + L.canon_token);
   pa.tok_slot = const_cast<int*>(pl.tok_slot);
-  pa.mt_flags = ws + L.mt_flags;
-  pa.mblocks1 = reinterpret_cast<int4*>(ws + L.mblocks1);
-  pa.mblocks2 = reinterpret_cast<int4*>(ws + L.mblocks2);
-  pa.mt1 = large_mt1(T);
-  pa.mt2 = large_mt2(T);
+  pa.mblocks = reinterpret_cast<int4*>(ws + L.mblocks);
+  pa.rows_a = large_rows_a(T, H);
+  pa.rows_b = large_rows_b(T, H);
   pl.canon_token = pa.canon_token;
-  pl.mt_flags = pa.mt_flags;
-  pl.mblocks1 = pa.mblocks1;
-  pl.mblocks2 = pa.mblocks2;
+  pl.mblocks = pa.mblocks;
   CHalf8 ch;
   ch.hi = reinterpret_cast<_Float16*>(ws + L.c_hi);
   ch.lo = ws + L.c_lo;
@@ -340,9 +337,14 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   mark(1);
   launch_permute_large(pa, s);
   mark(2);
-  launch_gemm1_large(pb, pl, ch, pa.mt1, (int)(L.max_mb1 * (I / kBlock)), s);
+  if (large_big(T, H)) {
+    launch_gemm1_big(pb, pl, ch, (int)(L.max_blocks_a * (I / kBlock)), s);
+    launch_gemm1_large(pb, pl, ch, kExactRows / 16, (int)((L.max_blocks - L.max_blocks_a) * (I / kBlock)), 1, s);
+  } else {
+    launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks * (I / kBlock)), 0, s);
+  }
   mark(3);
-  launch_gemm2_large(pb, pl, ch, obuf, pa.mt2, (int)(L.max_mb2 * (H / kBlock)), s);
+  launch_gemm2_large(pb, pl, ch, obuf, large_big(T, H) ? 4 : large_mt(T), (int)(L.max_blocks * (H / kBlock)), s);
   mark(4);
   launch_combine(pl, obuf, a->output, (int)T, H, s);
   mark(5);

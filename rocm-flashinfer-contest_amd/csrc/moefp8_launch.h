@@ -44,12 +44,13 @@ struct Plan {
   const int* tok_slot;        // [T * 8]
   const int* active;          // [E_local]
   const int* mtile_offsets;   // [E_local + 1]
-  const int* info;            // {P, n_active, m-blocks|m-tiles, S1, S2, GEMM2 m-blocks, m-tiles}
+  const int* info;            // {P, n_active, m-blocks|m-tiles, S1, S2, GEMM2 m-blocks, m-tiles, large T:
+                              //  class 0/1 m-blocks}
   const uint8_t* exact;       // small T: [Pmax] per-pair flags (kFlagExactProducts, kFlagTwoTermC)
   const int4* mtiles;         // small T: per m-tile {expert, first pair, rows, OR of pair flags}
-  const uint8_t* mt_flags;    // large T: per 16-row m-tile, OR of its pairs' flags
-  const int4* mblocks1;       // large T: GEMM1 m-blocks {expert, first row, rows, first m-tile}
-  const int4* mblocks2;       // large T: the same for GEMM2's m-block height
+  const int4* mblocks;        // large T: m-blocks {expert, first row, rows, OR of pair flags}, both GEMMs;
+                              // blocks of the expert's class 0/1 rows first (info[7] of them), then
+                              // blocks of its exact-product rows
   const int* canon_token;     // token of each pair in canonical (expert, token) order
 };
 
@@ -96,10 +97,9 @@ struct LargePermArgs {
   float* perm_w;        // [Pmax]
   int* canon_token;     // [Pmax] canonical order
   int* tok_slot;        // [T * 8] internal rows of each token's pairs, ascending expert
-  uint8_t* mt_flags;    // [max m-tiles]
-  int4* mblocks1;       // GEMM1 m-blocks of mt1 m-tiles
-  int4* mblocks2;       // GEMM2 m-blocks of mt2 m-tiles
-  int mt1, mt2;
+  int4* mblocks;        // [max blocks] {expert, first row, rows, flags}
+  int rows_a;           // block height over an expert's class 0 and 1 rows
+  int rows_b;           // block height over its class 2 (exact-product) rows
 };
 void launch_permute_large(const LargePermArgs& args, hipStream_t stream);
 int permute_large_blocks(int64_t T);
@@ -112,8 +112,14 @@ struct CHalf8 {
   float* scale;     // [Pmax][I/128]
 };
 int large_grid();
-void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units,
+// GEMM1 over blocks [0, info[2]) (from_exact = 0) or over the exact-product blocks
+// [info[7], info[2]) (from_exact = 1), 16 * mt rows per block
+void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units, int from_exact,
                         hipStream_t stream);
+// GEMM1 over the kBigRows-row class 0/1 blocks [0, info[7]), one workgroup per CU
+constexpr int kBigRows = 128;
+constexpr int kBigMaxKB = 64;   // H <= 8192
+void launch_gemm1_big(const Problem& pb, const Plan& pl, const CHalf8& ch, int max_units, hipStream_t stream);
 void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
                         hipStream_t stream);
 

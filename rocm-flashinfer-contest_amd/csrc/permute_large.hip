@@ -2,8 +2,8 @@
 // blocks of 256 tokens (one token per thread):
 //
 //   count  per block, the number of pairs in each bucket (local expert, magnitude class)
-//   scan   one workgroup: bucket and expert offsets, the 16-row m-tile flags and the
-//          m-block tables of both grouped GEMMs
+//   scan   one workgroup: bucket and expert offsets and the m-block table of the grouped
+//          GEMMs
 //   place  per block, each pair's rank inside its bucket in token order gives its row;
 //          the rank inside its expert alone gives its canonical row
 //
@@ -88,7 +88,7 @@ __device__ __forceinline__ int wave_exclusive_sum(int v) {
 
 __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a) {
   __shared__ int tot[kEGlobal * kClasses];
-  __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], emb1[kEGlobal + 1], emb2[kEGlobal + 1];
+  __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], eba[kEGlobal + 1], ebb[kEGlobal + 1];
   const int E = a.E_local, E3 = E * kClasses, nb = a.nblk, tid = threadIdx.x, lane = lane_id();
 
   // canonical per-block base of each expert (relative), from the raw counts
@@ -113,45 +113,49 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
     tot[i] = run;
   }
   __syncthreads();
+  // expert offsets, 16-row m-tile offsets and m-block offsets: blocks of rows_a rows over an
+  // expert's class 0 and 1 rows, blocks of rows_b rows over its class 2 rows
   if (tid < kWave) {
-    int carry = 0, carry_mt = 0, carry_mb1 = 0, carry_mb2 = 0, carry_act = 0;
+    int carry = 0, carry_mt = 0, carry_a = 0, carry_b = 0, carry_act = 0;
     for (int e0 = 0; e0 < E; e0 += kWave) {
       const int e = e0 + lane;
-      const int n = e < E ? tot[kClasses * e] + tot[kClasses * e + 1] + tot[kClasses * e + 2] : 0;
+      const int c01 = e < E ? tot[kClasses * e] + tot[kClasses * e + 1] : 0;
+      const int n = e < E ? c01 + tot[kClasses * e + 2] : 0;
       const int mt = (n + 15) / 16;
-      const int mb1 = (mt + a.mt1 - 1) / a.mt1, mb2 = (mt + a.mt2 - 1) / a.mt2;
+      const int ba = (c01 + a.rows_a - 1) / a.rows_a, bb = (n - c01 + a.rows_b - 1) / a.rows_b;
       const int pn = wave_exclusive_sum(n), pmt = wave_exclusive_sum(mt);
-      const int pmb1 = wave_exclusive_sum(mb1), pmb2 = wave_exclusive_sum(mb2);
+      const int pa = wave_exclusive_sum(ba), pb = wave_exclusive_sum(bb);
       const uint64_t act = __ballot(n > 0);
       if (e < E) {
         eoff[e] = carry + pn;
         emt[e] = carry_mt + pmt;
-        emb1[e] = carry_mb1 + pmb1;
-        emb2[e] = carry_mb2 + pmb2;
+        eba[e] = carry_a + pa;
+        ebb[e] = carry_b + pb;
         a.expert_offsets[e] = carry + pn;
         a.mtile_offsets[e] = carry_mt + pmt;
         if (n > 0) a.active[carry_act + lanes_below(act)] = e;
       }
       carry += __builtin_amdgcn_readlane(pn + n, kWave - 1);
       carry_mt += __builtin_amdgcn_readlane(pmt + mt, kWave - 1);
-      carry_mb1 += __builtin_amdgcn_readlane(pmb1 + mb1, kWave - 1);
-      carry_mb2 += __builtin_amdgcn_readlane(pmb2 + mb2, kWave - 1);
+      carry_a += __builtin_amdgcn_readlane(pa + ba, kWave - 1);
+      carry_b += __builtin_amdgcn_readlane(pb + bb, kWave - 1);
       carry_act += (int)__popcll(act);
     }
     if (lane == 0) {
       eoff[E] = carry;
       emt[E] = carry_mt;
-      emb1[E] = carry_mb1;
-      emb2[E] = carry_mb2;
+      eba[E] = carry_a;
+      ebb[E] = carry_b;
       a.expert_offsets[E] = carry;
       a.mtile_offsets[E] = carry_mt;
-      a.info[0] = carry;       // P
-      a.info[1] = carry_act;   // active experts
-      a.info[2] = carry_mb1;   // GEMM1 m-blocks
-      a.info[3] = 1;           // K-splits (small-T GEMMs only)
+      a.info[0] = carry;                // P
+      a.info[1] = carry_act;            // active experts
+      a.info[2] = carry_a + carry_b;    // m-blocks (both GEMMs)
+      a.info[3] = 1;                    // K-splits (small-T GEMMs only)
       a.info[4] = 1;
-      a.info[5] = carry_mb2;   // GEMM2 m-blocks
-      a.info[6] = carry_mt;    // 16-row m-tiles
+      a.info[5] = carry_a + carry_b;
+      a.info[6] = carry_mt;             // 16-row m-tiles
+      a.info[7] = carry_a;              // m-blocks over class 0/1 rows (they come first)
     }
   }
   __syncthreads();
@@ -162,27 +166,19 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
     a.bcnt[i] += base;
   }
   for (int i = tid; i < nb * E; i += kScanThreads) a.ccnt[i] += eoff[i % E];
-  // m-tile flags: OR of the classes whose rows meet the tile
-  for (int g = tid; g < emt[E]; g += kScanThreads) {
-    const int e = upper_bound(emt, E + 1, g) - 1;
-    const int r0 = (g - emt[e]) * 16, r1 = r0 + 16;
-    const int n = eoff[e + 1] - eoff[e];
-    const int c1 = tot[kClasses * e], c2 = c1 + tot[kClasses * e + 1];
-    uint8_t f = 0;
-    if (r0 < c2 && r1 > c1) f |= class_flags(1);
-    if (r1 > c2 && r0 < n) f |= class_flags(2);
-    a.mt_flags[g] = f;
+  // m-block table {expert, first row, rows, OR of the flags of its pairs' classes}
+  const int na = eba[E], nbk = ebb[E];
+  for (int g = tid; g < na; g += kScanThreads) {
+    const int e = upper_bound(eba, E + 1, g) - 1, j = g - eba[e];
+    const int c0 = tot[kClasses * e], c01 = c0 + tot[kClasses * e + 1], r0 = j * a.rows_a;
+    const int rows = min(a.rows_a, c01 - r0);
+    a.mblocks[g] = int4{e, eoff[e] + r0, rows, r0 + rows > c0 ? (int)class_flags(1) : 0};
   }
-  // m-block tables {expert, first row, rows, first m-tile}
-  for (int g = tid; g < emb1[E]; g += kScanThreads) {
-    const int e = upper_bound(emb1, E + 1, g) - 1, j = g - emb1[e];
-    const int n = eoff[e + 1] - eoff[e], r0 = j * 16 * a.mt1;
-    a.mblocks1[g] = int4{e, eoff[e] + r0, min(16 * a.mt1, n - r0), emt[e] + j * a.mt1};
-  }
-  for (int g = tid; g < emb2[E]; g += kScanThreads) {
-    const int e = upper_bound(emb2, E + 1, g) - 1, j = g - emb2[e];
-    const int n = eoff[e + 1] - eoff[e], r0 = j * 16 * a.mt2;
-    a.mblocks2[g] = int4{e, eoff[e] + r0, min(16 * a.mt2, n - r0), emt[e] + j * a.mt2};
+  for (int g = tid; g < nbk; g += kScanThreads) {
+    const int e = upper_bound(ebb, E + 1, g) - 1, j = g - ebb[e];
+    const int c01 = tot[kClasses * e] + tot[kClasses * e + 1], n = eoff[e + 1] - eoff[e];
+    const int r0 = c01 + j * a.rows_b;
+    a.mblocks[na + g] = int4{e, eoff[e] + r0, min(a.rows_b, n - r0), (int)class_flags(2)};
   }
 }
 

@@ -115,6 +115,7 @@ REDUCED = [
     (100, 4, 256, 128, -2),
     (50, 32, 256, 128, 300),
     (2500, 32, 256, 128, 0),
+    (2100, 16, 512, 256, 0),        # 128-row blocks with 4 K-blocks
 ]
 
 
@@ -143,7 +144,7 @@ def test_full_path_reduced_shapes(T, E_local, H, I, offset):
 
 
 @pytest.mark.parametrize("T,E_local,H,I", [(16, 8, 512, 256), (64, 32, 256, 256), (300, 16, 512, 256),
-                                              (1500, 32, 256, 128)])
+                                              (1500, 32, 256, 128), (2100, 16, 512, 256)])
 def test_full_path_high_magnitude_tokens(T, E_local, H, I):
     """Tokens with 30-120x hidden amplitude (outputs up to ~1e4) take the exact-product
     sub-tile path; every element must still meet atol 1e-2 / rtol 2e-2."""
