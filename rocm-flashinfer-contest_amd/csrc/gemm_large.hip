@@ -728,18 +728,20 @@ __device__ __forceinline__ void gemm2_large_store(const Plan& pl, float* __restr
   }
 }
 
-// Units (m-block, 128 output columns) over the whole block table; a block taller than 16 MT
-// rows (the 128-row class 0/1 blocks) is taken 16 MT rows at a time.
+// Units (m-block, 128 output columns) over blocks [first, info[5]) of the table, first = 0 or
+// info[7] (the exact-product blocks after the class 0/1 blocks that the 128-row kernel takes); a
+// block taller than 16 MT rows is taken 16 MT rows at a time.
 template <int MT>
 __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, Plan pl, CHalf8 ch,
-                                                                     float* __restrict__ obuf) {
+                                                                     float* __restrict__ obuf, int from_exact) {
   using L = G2L<MT>;
   constexpr int NP = MT / 2;
   __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
   const int H = pb.H, HB = H / kBlock;
-  const int n_units = pl.info[5] * HB;
+  const int mb_first = from_exact ? pl.info[7] : 0;
+  const int n_units = (pl.info[5] - mb_first) * HB;
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-    const int mb = u / HB, hb = u - mb * HB;
+    const int mb = mb_first + u / HB, hb = u % HB;
     const int4 blk = pl.mblocks[mb];
     const int e = uniform(blk.x), flags = uniform(blk.w);
     for (int s0 = 0; s0 < blk.z; s0 += 16 * MT) {
@@ -763,6 +765,178 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
         gemm2_large_store<MT>(pl, obuf, H, row0, rows, hb, 0, acc);
       }
     }
+  }
+}
+
+// ------------------------------------------------------------------------------ GEMM2, 128-row m-blocks
+// For the 128-row class 0 (one term of C) and class 1 (two terms) blocks.  A workgroup of 8
+// wavefronts (one per CU, two per SIMD) owns one unit = (m-block, 256 output columns) and stages
+// C's hi term (f16), its lo term (e4m3, two-term blocks) and the W2 rows by DMA through a 3-stage
+// LDS ring, 64 K per stage.  Wavefront (wm, wn) = (w % 2, w / 2) computes rows 64 wm .. +63 x
+// output columns 64 wn .. +63 on the f16 MFMA 16x16x32 (W2 widened to f16 exactly; the lo term
+// widened with its 2^-11 scale, also exact, and chained onto the hi products).
+//
+// Within a 64-K stage, lane group kg of an MFMA operand holds k = 16 kg + 8 t + (0..7) for the
+// two 32-K MFMAs t = 0, 1 (the same order for both operands): its W2 and lo bytes are one
+// 16-byte chunk, its hi values two.
+//
+// LDS stage: hi [128 rows][128 B] (chunks swizzled by bg_key), lo [128 rows][64 B] and W2
+// [256 rows][64 B] (chunk c of row r in slot c ^ bg_key4(r)), 128 row scales of C.
+constexpr int kB2Cols = 256;
+constexpr int kB2Hi = kBgRows * 128;
+constexpr int kB2Lo = kBgRows * 64;
+constexpr int kB2W = kB2Cols * 64;
+constexpr int kB2Stage = kB2Hi + kB2Lo + kB2W + kBgRows * 4;
+constexpr int kB2Stages = 3;
+
+// 4-slot swizzle of 64-byte rows: any 16 consecutive rows reading one chunk hit distinct 16-byte
+// bank groups of a 256-byte bank row, and any 8 (same row parity) of a 128-byte one.
+__device__ __forceinline__ int bg_key4(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
+
+// e4m3 x 16 -> two f16 x 8 (MFMA operand order k = 8t + 0..7), scaled exactly by 2^kExp
+__device__ __forceinline__ void widen16(const v4i& x, float scale, v8h& t0, v8h& t1) {
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    const uint32_t word = (uint32_t)x[w];
+    const v2h lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, scale, false);
+    const v2h hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, scale, true);
+    v8h& t = w < 2 ? t0 : t1;
+    const int o = 4 * (w & 1);
+    t[o + 0] = lo[0];
+    t[o + 1] = lo[1];
+    t[o + 2] = hi[0];
+    t[o + 3] = hi[1];
+  }
+}
+
+template <bool kTwo>
+__device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
+                                               uint32_t ring_lds, const float* sw2_s, int e, int row0, int rows,
+                                               int hc, float* __restrict__ obuf) {
+  constexpr int kOps = 2 + (kTwo ? 1 : 0) + 2 + 1;  // hi, lo, W2 and row-scale DMAs per wavefront
+  const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
+  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+  // DMA sources (per-lane byte offsets): hi rows 16w + 8q + (lane / 8), 8 slots per row; lo rows
+  // 16w + (lane / 4), W2 rows 32w + 16q + (lane / 4), 4 slots per row; row scales 64 (w % 2) + lane
+  uint32_t hoff[2], loff = 0, woff[2];
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int r = 16 * wave + 8 * q + (lane >> 3);
+    const int p = row0 + min(r, rows - 1);
+    hoff[q] = (uint32_t)p * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
+  }
+  if (kTwo) {
+    const int r = 16 * wave + (lane >> 2);
+    const int p = row0 + min(r, rows - 1);
+    loff = (uint32_t)p * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(r))) * 16);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int R = 32 * wave + 16 * q + (lane >> 2);
+    woff[q] = (uint32_t)(hc * kB2Cols + R) * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(R))) * 16);
+  }
+  const uint32_t soff = 4u * (uint32_t)((row0 + min(64 * (wave & 1) + lane, rows - 1)) * KB);
+  const uint8_t* wbase = pb.w2 + (size_t)e * H * I;
+  auto issue = [&](int j) {
+    const int k = min(j, KS - 1);
+    const uint32_t st = ring_lds + (uint32_t)((j % kB2Stages) * kB2Stage);
+    const uint8_t* hbase = reinterpret_cast<const uint8_t*>(ch.hi) + (size_t)k * 128;
+#pragma unroll
+    for (int q = 0; q < 2; q++) dma_lds16_s(hoff[q], hbase, st + (16 * wave + 8 * q) * 128);
+    if (kTwo) dma_lds16_s(loff, ch.lo + (size_t)k * 64, st + kB2Hi + 16 * wave * 64);
+#pragma unroll
+    for (int q = 0; q < 2; q++) dma_lds16_s(woff[q], wbase + (size_t)k * 64, st + kB2Hi + kB2Lo + (32 * wave + 16 * q) * 64);
+    dma_lds4_s(soff, ch.scale + k / 2, st + kB2Hi + kB2Lo + kB2W + (wave & 1) * 256);
+  };
+  // operand read offsets: hi chunks 2kg + t of row lr (bg_key), lo / W2 chunk kg of row lr (bg_key4)
+  const int rh0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
+  const int rh1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
+  const int rq = lr * 64 + ((kg ^ bg_key4(lr)) * 16);
+
+  MOEFP8_WAIT_VMCNT(0);
+  for (int d = 0; d < kB2Stages - 1; d++) issue(d);
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < KS; j++) {
+    static_assert(kB2Stages == 3, "one stage in flight past the current one");
+    if (kTwo) MOEFP8_WAIT_VMCNT(6);
+    else MOEFP8_WAIT_VMCNT(5);
+    barrier_lds();
+    const uint8_t* st = ring + (j % kB2Stages) * kB2Stage;
+    v8h b16[4][2];
+#pragma unroll
+    for (int n = 0; n < 4; n++)
+      widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + kB2Lo + (64 * wn + 16 * n) * 64 + rq), 1.0f, b16[n][0],
+              b16[n][1]);
+    const float sw = sw2_s[(j / 2) * 2 + (wn >> 1)];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int t = 4 * wm + i;
+      const uint8_t* ht = st + t * 16 * 128;
+      const v8h a0 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh0));
+      const v8h a1 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh1));
+      v8h l0 = {}, l1 = {};
+      if constexpr (kTwo)
+        widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + t * 16 * 64 + rq), 1.0f / kLoScale, l0, l1);
+      const float4 sa = *reinterpret_cast<const float4*>(st + kB2Hi + kB2Lo + kB2W + (16 * t + 4 * kg) * 4);
+      const float4 sc = {sa.x * sw, sa.y * sw, sa.z * sw, sa.w * sw};
+#pragma unroll
+      for (int n = 0; n < 4; n++) {
+        v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b16[n][0], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b16[n][1], p, 0, 0, 0);
+        if constexpr (kTwo) {
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, b16[n][0], p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, b16[n][1], p, 0, 0, 0);
+        }
+        acc[i][n][0] += p[0] * sc.x;
+        acc[i][n][1] += p[1] * sc.y;
+        acc[i][n][2] += p[2] * sc.z;
+        acc[i][n][3] += p[3] * sc.w;
+      }
+    }
+    issue(j + kB2Stages - 1);
+  }
+  MOEFP8_WAIT_VMCNT(0);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int row = 16 * (4 * wm + i) + 4 * kg + r;
+      if (row < rows) {
+        const int p = row0 + row;
+        const float w = pl.perm_w[p];
+#pragma unroll
+        for (int n = 0; n < 4; n++) obuf[(size_t)p * H + hc * kB2Cols + 64 * wn + 16 * n + lr] = acc[i][n][r] * w;
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Plan pl, CHalf8 ch,
+                                                                 float* __restrict__ obuf) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kB2Stages * kB2Stage];
+  __shared__ float sw2_s[2 * kBigMaxKB];
+  const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock, HC = H / kB2Cols;
+  const int n_units = pl.info[7] * HC;
+  const uint32_t ring_lds = uniform((int)lds_addr(ring));
+  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const int mb = u / HC, hc = u % HC;
+    const int4 blk = pl.mblocks[mb];
+    const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
+    // the previous unit's readers are done with the ring and sw2_s
+    __syncthreads();
+    // W2 block scales of the unit's two 128-column blocks, per 128-K block
+    {
+      const int t = threadIdx.x;
+      if (t < 2 * KB) sw2_s[t] = pb.s2[((size_t)e * HB + 2 * hc + (t & 1)) * KB + (t >> 1)];
+    }
+    __syncthreads();
+    if (flags & kFlagTwoTermC) gemm2_big_unit<true>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+    else gemm2_big_unit<false>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
   }
 }
 
@@ -792,13 +966,27 @@ void launch_gemm1_big(const Problem& pb, const Plan& pl, const CHalf8& ch, int m
 }
 
 void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
-                        hipStream_t stream) {
+                        int from_exact, hipStream_t stream) {
   const int grid = max_units < large_grid() ? max_units : large_grid();
   if (grid <= 0) return;
   switch (mt) {
-    case 2: hipLaunchKernelGGL(gemm2_large_kernel<2>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, obuf); break;
-    default: hipLaunchKernelGGL(gemm2_large_kernel<4>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, obuf); break;
+    case 2:
+      hipLaunchKernelGGL(gemm2_large_kernel<2>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, obuf,
+                         from_exact);
+      break;
+    default:
+      hipLaunchKernelGGL(gemm2_large_kernel<4>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, obuf,
+                         from_exact);
+      break;
   }
+}
+
+void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int max_units,
+                      hipStream_t stream) {
+  const int cus = num_compute_units();
+  const int grid = max_units < cus ? max_units : cus;
+  if (grid <= 0) return;
+  hipLaunchKernelGGL(gemm2_big_kernel, dim3(grid), dim3(kBgThreads), 0, stream, pb, pl, ch, obuf);
 }
 
 }  // namespace moefp8

@@ -26,10 +26,13 @@ constexpr int64_t kDecodeMaxT = 64;
 constexpr int64_t kBigT = 2048;
 constexpr int kExactRows = 32;
 // (the 128-row GEMM1 addresses hidden rows with 32-bit byte offsets)
-bool large_big(int64_t T, int H) { return T >= kBigT && H / kBlock <= kBigMaxKB && T * H < ((int64_t)1 << 31); }
+bool large_big(int64_t T, int H, int I) {
+  return T >= kBigT && H / kBlock <= kBigMaxKB && I / kBlock <= kBigMaxKB && H % 256 == 0 &&
+         T * H < ((int64_t)1 << 31);
+}
 int large_mt(int64_t T) { return T / 32 >= 48 ? 4 : 2; }
-int large_rows_a(int64_t T, int H) { return large_big(T, H) ? kBigRows : 16 * large_mt(T); }
-int large_rows_b(int64_t T, int H) { return large_big(T, H) ? kExactRows : 16 * large_mt(T); }
+int large_rows_a(int64_t T, int H, int I) { return large_big(T, H, I) ? kBigRows : 16 * large_mt(T); }
+int large_rows_b(int64_t T, int H, int I) { return large_big(T, H, I) ? kExactRows : 16 * large_mt(T); }
 
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
@@ -82,8 +85,8 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   // large T: permutation scratch and tables, C (f16 hi, e4m3 or f16 lo, fp32 scales), O [pmax][H] fp32
   L.rows_cap = pmax;
   L.nblk = permute_large_blocks(T);
-  const int ra = large_rows_a(T, H), rb = large_rows_b(T, H);
-  L.max_blocks_a = (pmax + ra - 1) / ra + E_local;
+  const int ra = large_rows_a(T, H, I), rb = large_rows_b(T, H, I);
+  L.max_blocks_a = (pmax + ra - 1) / ra + 2 * E_local;   // class 0 and class 1 blocks per expert
   L.max_blocks = L.max_blocks_a + (pmax + rb - 1) / rb + E_local;
   L.canon_token = take((size_t)pmax * 4);
   L.bcnt = take((size_t)L.nblk * E_local * 3 * 4);
@@ -321,8 +324,8 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pa.canon_token = reinterpret_cast<int*>(ws + L.canon_token);
   pa.tok_slot = const_cast<int*>(pl.tok_slot);
   pa.mblocks = reinterpret_cast<int4*>(ws + L.mblocks);
-  pa.rows_a = large_rows_a(T, H);
-  pa.rows_b = large_rows_b(T, H);
+  pa.rows_a = large_rows_a(T, H, I);
+  pa.rows_b = large_rows_b(T, H, I);
   pl.canon_token = pa.canon_token;
   pl.mblocks = pa.mblocks;
   CHalf8 ch;
@@ -337,14 +340,19 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   mark(1);
   launch_permute_large(pa, s);
   mark(2);
-  if (large_big(T, H)) {
+  if (large_big(T, H, I)) {
     launch_gemm1_big(pb, pl, ch, (int)(L.max_blocks_a * (I / kBlock)), s);
     launch_gemm1_large(pb, pl, ch, kExactRows / 16, (int)((L.max_blocks - L.max_blocks_a) * (I / kBlock)), 1, s);
   } else {
     launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks * (I / kBlock)), 0, s);
   }
   mark(3);
-  launch_gemm2_large(pb, pl, ch, obuf, large_big(T, H) ? 4 : large_mt(T), (int)(L.max_blocks * (H / kBlock)), s);
+  if (large_big(T, H, I)) {
+    launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks_a * (H / 256)), s);
+    launch_gemm2_large(pb, pl, ch, obuf, kExactRows / 16, (int)((L.max_blocks - L.max_blocks_a) * (H / kBlock)), 1, s);
+  } else {
+    launch_gemm2_large(pb, pl, ch, obuf, large_mt(T), (int)(L.max_blocks * (H / kBlock)), 0, s);
+  }
   mark(4);
   launch_combine(pl, obuf, a->output, (int)T, H, s);
   mark(5);

@@ -120,8 +120,13 @@ void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int
 constexpr int kBigRows = 128;
 constexpr int kBigMaxKB = 64;   // H <= 8192
 void launch_gemm1_big(const Problem& pb, const Plan& pl, const CHalf8& ch, int max_units, hipStream_t stream);
+// GEMM2 over blocks [0, info[5]) (from_exact = 0) or over the exact-product blocks
+// [info[7], info[5]) (from_exact = 1), blocks taken 16 * mt rows at a time
 void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
-                        hipStream_t stream);
+                        int from_exact, hipStream_t stream);
+// GEMM2 over the kBigRows-row class 0/1 blocks [0, info[7]), 256 output columns per unit
+void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int max_units,
+                      hipStream_t stream);
 
 void launch_combine(const Plan& pl, const float* obuf, uint16_t* out, int T, int H, hipStream_t stream);
 

@@ -114,15 +114,17 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
   }
   __syncthreads();
   // expert offsets, 16-row m-tile offsets and m-block offsets: blocks of rows_a rows over an
-  // expert's class 0 and 1 rows, blocks of rows_b rows over its class 2 rows
+  // expert's class 0 rows, then over its class 1 rows (blocks of one precision mode each), blocks
+  // of rows_b rows over its class 2 rows
   if (tid < kWave) {
     int carry = 0, carry_mt = 0, carry_a = 0, carry_b = 0, carry_act = 0;
     for (int e0 = 0; e0 < E; e0 += kWave) {
       const int e = e0 + lane;
-      const int c01 = e < E ? tot[kClasses * e] + tot[kClasses * e + 1] : 0;
-      const int n = e < E ? c01 + tot[kClasses * e + 2] : 0;
+      const int n0 = e < E ? tot[kClasses * e] : 0, n1 = e < E ? tot[kClasses * e + 1] : 0;
+      const int n2 = e < E ? tot[kClasses * e + 2] : 0, n = n0 + n1 + n2;
       const int mt = (n + 15) / 16;
-      const int ba = (c01 + a.rows_a - 1) / a.rows_a, bb = (n - c01 + a.rows_b - 1) / a.rows_b;
+      const int ba = (n0 + a.rows_a - 1) / a.rows_a + (n1 + a.rows_a - 1) / a.rows_a;
+      const int bb = (n2 + a.rows_b - 1) / a.rows_b;
       const int pn = wave_exclusive_sum(n), pmt = wave_exclusive_sum(mt);
       const int pa = wave_exclusive_sum(ba), pb = wave_exclusive_sum(bb);
       const uint64_t act = __ballot(n > 0);
@@ -155,7 +157,7 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
       a.info[4] = 1;
       a.info[5] = carry_a + carry_b;
       a.info[6] = carry_mt;             // 16-row m-tiles
-      a.info[7] = carry_a;              // m-blocks over class 0/1 rows (they come first)
+      a.info[7] = carry_a;              // m-blocks over class 0 and 1 rows (they come first)
     }
   }
   __syncthreads();
@@ -166,13 +168,16 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
     a.bcnt[i] += base;
   }
   for (int i = tid; i < nb * E; i += kScanThreads) a.ccnt[i] += eoff[i % E];
-  // m-block table {expert, first row, rows, OR of the flags of its pairs' classes}
+  // m-block table {expert, first row, rows, flags of the block's class}
   const int na = eba[E], nbk = ebb[E];
   for (int g = tid; g < na; g += kScanThreads) {
     const int e = upper_bound(eba, E + 1, g) - 1, j = g - eba[e];
-    const int c0 = tot[kClasses * e], c01 = c0 + tot[kClasses * e + 1], r0 = j * a.rows_a;
-    const int rows = min(a.rows_a, c01 - r0);
-    a.mblocks[g] = int4{e, eoff[e] + r0, rows, r0 + rows > c0 ? (int)class_flags(1) : 0};
+    const int n0 = tot[kClasses * e], n1 = tot[kClasses * e + 1];
+    const int b0 = (n0 + a.rows_a - 1) / a.rows_a;
+    const int c = j < b0 ? 0 : 1;
+    const int r0 = c == 0 ? j * a.rows_a : n0 + (j - b0) * a.rows_a;
+    const int end = c == 0 ? n0 : n0 + n1;
+    a.mblocks[g] = int4{e, eoff[e] + r0, min(a.rows_a, end - r0), (int)class_flags(c)};
   }
   for (int g = tid; g < nbk; g += kScanThreads) {
     const int e = upper_bound(ebb, E + 1, g) - 1, j = g - ebb[e];
