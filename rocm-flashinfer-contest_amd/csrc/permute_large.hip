@@ -252,10 +252,11 @@ __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a)
   wave_key_ranks(ek, re, wcan[wave]);
   __syncthreads();
   if (!in) return;
-  int kk = 0;
+  int n_local = 0;
 #pragma unroll
   for (int k = 0; k < kTopK; k++) {
     if (bk[k] < 0) continue;
+    n_local++;
     int pos = a.bcnt[(size_t)blockIdx.x * E3 + bk[k]] + rb[k];
     int cpos = a.ccnt[(size_t)blockIdx.x * E + ek[k]] + re[k];
     for (int w = 0; w < wave; w++) {
@@ -265,10 +266,14 @@ __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a)
     a.perm_token[pos] = t;
     a.perm_w[pos] = wk[k];
     a.canon_token[cpos] = t;
-    a.tok_slot[(size_t)t * kTopK + kk] = pos;
-    kk++;
+    // slot = rank of the local expert among the token's local experts: the combine adds a
+    // token's rows in ascending expert order
+    int slot = 0;
+#pragma unroll
+    for (int q = 0; q < kTopK; q++) slot += (ek[q] >= 0 && ek[q] < ek[k]) ? 1 : 0;
+    a.tok_slot[(size_t)t * kTopK + slot] = pos;
   }
-  for (; kk < kTopK; kk++) a.tok_slot[(size_t)t * kTopK + kk] = -1;
+  for (int kk = n_local; kk < kTopK; kk++) a.tok_slot[(size_t)t * kTopK + kk] = -1;
 }
 
 void launch_permute_large(const LargePermArgs& args, hipStream_t stream) {

@@ -353,11 +353,17 @@ __global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
   }
   __syncthreads();
 
-  // k = rank of this pair among its token's local pairs (a wave holds 8 whole tokens)
+  // k = rank of this pair's local expert among its token's local experts (a wave holds 8 whole
+  // tokens, lanes 8t'..8t'+7): the combine adds a token's rows in ascending expert order
   const uint32_t tb = (uint32_t)(__ballot(local) >> (8 * (lane >> 3))) & 0xffu;
   const int n = __popc(tb);
+  int k = 0;
+#pragma unroll
+  for (int q = 0; q < kTopK; q++) {
+    const int le_q = __shfl(local ? le : kEGlobal, (lane & ~7) + q, kWave);
+    k += le_q < le ? 1 : 0;
+  }
   if (local) {
-    const int k = __popc(tb & ((1u << j) - 1u));
     const int pos = base_s[le] + (int)__popcll(tmask[le] & ((1ull << t) - 1ull));
     perm_token[pos] = t;
     perm_w[pos] = w;
