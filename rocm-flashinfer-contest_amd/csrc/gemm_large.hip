@@ -399,59 +399,172 @@ constexpr int kBgOps = 2 + 4 + 1;            // per wavefront and K-block: A, B 
 
 __device__ __forceinline__ int bg_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-__global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Plan pl, CHalf8 ch) {
-  __shared__ __attribute__((aligned(16))) uint8_t ring[kBgStages * kBgStage];
-  __shared__ __attribute__((aligned(16))) float2 sw_s[kBigMaxKB];
-  __shared__ float amax_s[4][kBgRows];
+// One unit.  kExact (blocks of at most 32 exact-product rows): wavefront (wm, wn) takes m-tile wm
+// alone, on the f16 MFMA with operands widened exactly, and C's lo term is written in f16.
+template <bool kExact>
+__device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
+                                               uint32_t ring_lds, const float2* sw_s, float (*amax_s)[kBgRows],
+                                               int e, int row0, int rows, int cb, int flags) {
+  constexpr int NT = kExact ? 1 : 4;    // m-tiles per wavefront
   const int H = pb.H, I = pb.I, T = pb.T, KB = H / kBlock, NCB = I / kBlock;
   const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
-  const int n_units = pl.info[7] * NCB;
   // DMA lane roles: row (lane / 8) of an 8-row group, slot lane % 8
   const int drow = lane >> 3, dslot = lane & 7;
   // operand read offsets inside a 16-row tile (swizzled chunks 2kg and 2kg + 1 of row lr)
   const int rd0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
   const int rd1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
-  const uint32_t ring_lds = uniform((int)lds_addr(ring));
+  // DMA sources as per-lane byte offsets from wave-uniform bases: A rows 16w + 8q + drow (the
+  // tokens' hidden rows, clamped to the block), B LDS rows 32w + 8q + drow (LDS row R holds n-tile
+  // (R % 64) / 16 of weight-row group R / 64: 0, 1 up, 2, 3 gate), row scales of rows 64 (w % 2) + lane
+  uint32_t aoff[2], boff[4];
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int r = 16 * wave + 8 * q + drow;
+    const int tok = pl.perm_token[row0 + min(r, rows - 1)];
+    aoff[q] = (uint32_t)tok * (uint32_t)H + (uint32_t)((dslot ^ bg_key(r)) * 16);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int R = 32 * wave + 8 * q + drow;
+    const int g = R >> 6, n = (R >> 4) & 3, rr = R & 15;
+    const int wrow = (n < 2 ? 0 : I) + cb * kBlock + 32 * g + 16 * (n & 1) + rr;
+    boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ bg_key(R)) * 16);
+  }
+  const uint32_t soff = 4u * (uint32_t)pl.perm_token[row0 + min(64 * (wave & 1) + lane, rows - 1)];
+  const uint8_t* wbase = pb.w13 + (size_t)e * 2 * I * H;
+  auto issue = [&](int j) {
+    const int k = min(j, KB - 1);
+    const uint32_t st = ring_lds + (uint32_t)((j % kBgStages) * kBgStage);
+    const uint8_t* abase = pb.hidden + (size_t)k * kBlock;
+    const uint8_t* bbase = wbase + (size_t)k * kBlock;
+    const float* sbase = pb.hscale + (size_t)k * T;
+#pragma unroll
+    for (int q = 0; q < 2; q++) dma_lds16_s(aoff[q], abase, st + (16 * wave + 8 * q) * 128);
+#pragma unroll
+    for (int q = 0; q < 4; q++) dma_lds16_s(boff[q], bbase, st + kBgA + (32 * wave + 8 * q) * 128);
+    // wavefronts 2..7 repeat the row scales of 0 and 1 (same bytes), so that every wavefront
+    // issues the same operations
+    dma_lds4_s(soff, sbase, st + kBgA + kBgB + (wave & 1) * 256);
+  };
 
+  // the table and scale loads of the unit are complete: only DMAs count from here
+  MOEFP8_WAIT_VMCNT(0);
+  for (int d = 0; d < kBgStages - 1; d++) issue(d);
+  v4f acc[NT][4];
+#pragma unroll
+  for (int i = 0; i < NT; i++)
+#pragma unroll
+    for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  for (int j = 0; j < KB; j++) {
+    // stage j's DMAs are done once only the following stage's (7 per wavefront) may be in flight
+    static_assert((kBgStages - 2) * kBgOps == 7, "wait count");
+    MOEFP8_WAIT_VMCNT(7);
+    barrier_lds();
+    const uint8_t* st = ring + (j % kBgStages) * kBgStage;
+    v8i B[4];
+#pragma unroll
+    for (int n = 0; n < 4; n++) {
+      const uint8_t* bt = st + kBgA + (64 * wn + 16 * n) * 128;
+      B[n] = cat(*reinterpret_cast<const v4i*>(bt + rd0), *reinterpret_cast<const v4i*>(bt + rd1));
+    }
+    const float2 sw = sw_s[j];
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+      const int t = kExact ? wm : 4 * wm + i;
+      const uint8_t* at = st + t * 16 * 128;
+      const v8i a = cat(*reinterpret_cast<const v4i*>(at + rd0), *reinterpret_cast<const v4i*>(at + rd1));
+      const float4 sa = *reinterpret_cast<const float4*>(st + kBgA + kBgB + (16 * t + 4 * kg) * 4);
+      const float4 su = {sa.x * sw.x, sa.y * sw.x, sa.z * sw.x, sa.w * sw.x};
+      const float4 sg = {sa.x * sw.y, sa.y * sw.y, sa.z * sw.y, sa.w * sw.y};
+      v8h a16[4];
+      if constexpr (kExact) widen_fp8_operand(a, a16);
+#pragma unroll
+      for (int n = 0; n < 4; n++) {
+        const float4 sc = n < 2 ? su : sg;
+        v4f p;
+        if constexpr (kExact) {
+          v8h b16[4];
+          widen_fp8_operand(B[n], b16);
+          p = mfma_f16_block(a16, b16, v4f{0.f, 0.f, 0.f, 0.f});
+        } else {
+          p = mfma16x16x128(a, B[n], v4f{0.f, 0.f, 0.f, 0.f});
+        }
+        acc[i][n][0] += p[0] * sc.x;
+        acc[i][n][1] += p[1] * sc.y;
+        acc[i][n][2] += p[2] * sc.z;
+        acc[i][n][3] += p[3] * sc.w;
+      }
+    }
+    // stage (j + 2) % 3 was last read at step j - 1, before this step's barrier
+    issue(j + kBgStages - 1);
+  }
+  MOEFP8_WAIT_VMCNT(0);
+
+  // epilogue: C = silu(gate) * up, per-row max over the unit's 128 columns, hi/lo split
+  const int col0 = cb * kBlock + 32 * wn;
+  float c[NT][2][4];
+#pragma unroll
+  for (int i = 0; i < NT; i++)
+#pragma unroll
+    for (int jn = 0; jn < 2; jn++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) c[i][jn][r] = silu_f32(acc[i][jn + 2][r]) * acc[i][jn][r];
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const int t = kExact ? wm : 4 * wm + i;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float m = fmaxf(fabsf(c[i][0][r]), fabsf(c[i][1][r]));
+      m = fmaxf(m, dpp_f32<kDppXor1>(m));
+      m = fmaxf(m, dpp_f32<kDppXor2>(m));
+      m = fmaxf(m, dpp_f32<kDppHalfMirror>(m));
+      m = fmaxf(m, dpp_f32<kDppRowMirror>(m));
+      if (lr == 0) amax_s[wn][16 * t + 4 * kg + r] = m;
+    }
+  }
+  __syncthreads();
+  const bool two = (flags & kFlagTwoTermC) != 0;
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const int t = kExact ? wm : 4 * wm + i;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int row = 16 * t + 4 * kg + r;
+      if (row >= rows) continue;
+      const float amax = fmaxf(fmaxf(amax_s[0][row], amax_s[1][row]), fmaxf(amax_s[2][row], amax_s[3][row]));
+      float inv, scale;
+      split_scale(amax, inv, scale);
+      const size_t p = (size_t)(row0 + row);
+#pragma unroll
+      for (int jn = 0; jn < 2; jn++) {
+        const int col = col0 + 16 * jn + lr;
+        const float v = fminf(fmaxf(c[i][jn][r] * inv, -448.0f), 448.0f);
+        const _Float16 hi = (_Float16)v;
+        ch.hi[p * I + col] = hi;
+        if constexpr (kExact) ch.lo16[p * I + col] = (_Float16)(v - (float)hi);
+        else if (two)
+          ch.lo[p * I + col] = (uint8_t)f32_to_e4m3(fminf(fmaxf((v - (float)hi) * kLoScale, -448.0f), 448.0f));
+      }
+      if (wn == 0 && lr == 0) ch.scale[p * NCB + cb] = scale;
+    }
+  }
+}
+
+// Units (m-block, 128 C columns) over the whole block table: the 128-row class 0/1 blocks, then
+// the exact-product blocks.
+__global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Plan pl, CHalf8 ch) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kBgStages * kBgStage];
+  __shared__ __attribute__((aligned(16))) float2 sw_s[kBigMaxKB];
+  __shared__ float amax_s[4][kBgRows];
+  const int H = pb.H, I = pb.I, KB = H / kBlock, NCB = I / kBlock;
+  const int n_units = pl.info[2] * NCB;
+  const uint32_t ring_lds = uniform((int)lds_addr(ring));
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
     const int mb = u / NCB, cb = u % NCB;
     const int4 blk = pl.mblocks[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
-    // DMA sources as per-lane byte offsets from wave-uniform bases: A rows 16w + 8q + drow (the
-    // tokens' hidden rows), B LDS rows 32w + 8q + drow (LDS row R holds n-tile (R % 64) / 16 of
-    // weight-row group R / 64: 0, 1 up, 2, 3 gate), row scales of rows 64 (w % 2) + lane
-    uint32_t aoff[2], boff[4];
-#pragma unroll
-    for (int q = 0; q < 2; q++) {
-      const int r = 16 * wave + 8 * q + drow;
-      const int tok = pl.perm_token[row0 + min(r, rows - 1)];
-      aoff[q] = (uint32_t)tok * (uint32_t)H + (uint32_t)((dslot ^ bg_key(r)) * 16);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const int R = 32 * wave + 8 * q + drow;
-      const int g = R >> 6, n = (R >> 4) & 3, rr = R & 15;
-      const int wrow = (n < 2 ? 0 : I) + cb * kBlock + 32 * g + 16 * (n & 1) + rr;
-      boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ bg_key(R)) * 16);
-    }
-    const uint32_t soff = 4u * (uint32_t)pl.perm_token[row0 + min(64 * (wave & 1) + lane, rows - 1)];
-    const uint8_t* wbase = pb.w13 + (size_t)e * 2 * I * H;
-    auto issue = [&](int j) {
-      const int k = min(j, KB - 1);
-      const uint32_t st = ring_lds + (uint32_t)((j % kBgStages) * kBgStage);
-      const uint8_t* abase = pb.hidden + (size_t)k * kBlock;
-      const uint8_t* bbase = wbase + (size_t)k * kBlock;
-      const float* sbase = pb.hscale + (size_t)k * T;
-#pragma unroll
-      for (int q = 0; q < 2; q++) dma_lds16_s(aoff[q], abase, st + (16 * wave + 8 * q) * 128);
-#pragma unroll
-      for (int q = 0; q < 4; q++) dma_lds16_s(boff[q], bbase, st + kBgA + (32 * wave + 8 * q) * 128);
-      // wavefronts 2..7 repeat the row scales of 0 and 1 (same bytes), so that every wavefront
-      // issues the same operations
-      dma_lds4_s(soff, sbase, st + kBgA + kBgB + (wave & 1) * 256);
-    };
-
     // the previous unit's readers are done with the ring, amax_s and sw_s
     __syncthreads();
     // weight scales of the unit: {up, gate} per K-block
@@ -462,96 +575,10 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Pl
       if (t < KB) sw_s[t] = float2{su[t], sg[t]};
     }
     __syncthreads();
-    // the table and scale loads above are complete: only DMAs count from here
-    MOEFP8_WAIT_VMCNT(0);
-    for (int d = 0; d < kBgStages - 1; d++) issue(d);
-    v4f acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
-
-    for (int j = 0; j < KB; j++) {
-      // stage j's DMAs are done once only the following stage's (7 per wavefront) may be in flight
-      static_assert((kBgStages - 2) * kBgOps == 7, "wait count");
-      MOEFP8_WAIT_VMCNT(7);
-      barrier_lds();
-      const uint8_t* st = ring + (j % kBgStages) * kBgStage;
-      v8i B[4];
-#pragma unroll
-      for (int n = 0; n < 4; n++) {
-        const uint8_t* bt = st + kBgA + (64 * wn + 16 * n) * 128;
-        B[n] = cat(*reinterpret_cast<const v4i*>(bt + rd0), *reinterpret_cast<const v4i*>(bt + rd1));
-      }
-      const float2 sw = sw_s[j];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int t = 4 * wm + i;
-        const uint8_t* at = st + t * 16 * 128;
-        const v8i a = cat(*reinterpret_cast<const v4i*>(at + rd0), *reinterpret_cast<const v4i*>(at + rd1));
-        const float4 sa = *reinterpret_cast<const float4*>(st + kBgA + kBgB + (16 * t + 4 * kg) * 4);
-        const float4 su = {sa.x * sw.x, sa.y * sw.x, sa.z * sw.x, sa.w * sw.x};
-        const float4 sg = {sa.x * sw.y, sa.y * sw.y, sa.z * sw.y, sa.w * sw.y};
-#pragma unroll
-        for (int n = 0; n < 4; n++) {
-          const float4 sc = n < 2 ? su : sg;
-          const v4f p = mfma16x16x128(a, B[n], v4f{0.f, 0.f, 0.f, 0.f});
-          acc[i][n][0] += p[0] * sc.x;
-          acc[i][n][1] += p[1] * sc.y;
-          acc[i][n][2] += p[2] * sc.z;
-          acc[i][n][3] += p[3] * sc.w;
-        }
-      }
-      // stage (j + 2) % 3 was last read at step j - 1, before this step's barrier
-      issue(j + kBgStages - 1);
-    }
-    MOEFP8_WAIT_VMCNT(0);
-
-    // epilogue: C = silu(gate) * up, per-row max over the unit's 128 columns, hi/lo split
-    const int col0 = cb * kBlock + 32 * wn;
-    float c[4][2][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int jn = 0; jn < 2; jn++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) c[i][jn][r] = silu_f32(acc[i][jn + 2][r]) * acc[i][jn][r];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        float m = fmaxf(fabsf(c[i][0][r]), fabsf(c[i][1][r]));
-        m = fmaxf(m, dpp_f32<kDppXor1>(m));
-        m = fmaxf(m, dpp_f32<kDppXor2>(m));
-        m = fmaxf(m, dpp_f32<kDppHalfMirror>(m));
-        m = fmaxf(m, dpp_f32<kDppRowMirror>(m));
-        if (lr == 0) amax_s[wn][16 * (4 * wm + i) + 4 * kg + r] = m;
-      }
-    }
-    __syncthreads();
-    const bool two = (flags & kFlagTwoTermC) != 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int row = 16 * (4 * wm + i) + 4 * kg + r;
-        if (row >= rows) continue;
-        const float amax = fmaxf(fmaxf(amax_s[0][row], amax_s[1][row]), fmaxf(amax_s[2][row], amax_s[3][row]));
-        float inv, scale;
-        split_scale(amax, inv, scale);
-        const size_t p = (size_t)(row0 + row);
-#pragma unroll
-        for (int jn = 0; jn < 2; jn++) {
-          const int col = col0 + 16 * jn + lr;
-          const float v = fminf(fmaxf(c[i][jn][r] * inv, -448.0f), 448.0f);
-          const _Float16 hi = (_Float16)v;
-          ch.hi[p * I + col] = hi;
-          if (two)
-            ch.lo[p * I + col] = (uint8_t)f32_to_e4m3(fminf(fmaxf((v - (float)hi) * kLoScale, -448.0f), 448.0f));
-        }
-        if (wn == 0 && lr == 0) ch.scale[p * NCB + cb] = scale;
-      }
-    }
+    if (flags & kFlagExactProducts)
+      gemm1_big_unit<true>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
+    else
+      gemm1_big_unit<false>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
   }
 }
 
@@ -809,16 +836,20 @@ __device__ __forceinline__ void widen16(const v4i& x, float scale, v8h& t0, v8h&
   }
 }
 
-template <bool kTwo>
+// One unit.  kMode: kOneTerm / kTwoTerms (128-row blocks, 4 m-tiles per wavefront), kPrecise
+// (blocks of at most 32 exact-product rows: wavefront (wm, wn) takes m-tile wm with C's hi and
+// f16 lo terms, the lo rows staged in the stage's lo region as [32 rows][128 B]).
+template <int kMode>
 __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float* sw2_s, int e, int row0, int rows,
                                                int hc, float* __restrict__ obuf) {
-  constexpr int kOps = 2 + (kTwo ? 1 : 0) + 2 + 1;  // hi, lo, W2 and row-scale DMAs per wavefront
+  constexpr int NT = kMode == kPrecise ? 1 : 4;
   const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
   const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
-  // DMA sources (per-lane byte offsets): hi rows 16w + 8q + (lane / 8), 8 slots per row; lo rows
-  // 16w + (lane / 4), W2 rows 32w + 16q + (lane / 4), 4 slots per row; row scales 64 (w % 2) + lane
+  // DMA sources (per-lane byte offsets): hi rows 16w + 8q + (lane / 8), 8 slots per row; e4m3 lo
+  // rows 16w + (lane / 4), W2 rows 32w + 16q + (lane / 4), 4 slots per row; f16 lo rows
+  // 8 (w % 4) + (lane / 8); row scales 64 (w % 2) + lane
   uint32_t hoff[2], loff = 0, woff[2];
 #pragma unroll
   for (int q = 0; q < 2; q++) {
@@ -826,10 +857,14 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
     const int p = row0 + min(r, rows - 1);
     hoff[q] = (uint32_t)p * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
   }
-  if (kTwo) {
+  if (kMode == kTwoTerms) {
     const int r = 16 * wave + (lane >> 2);
     const int p = row0 + min(r, rows - 1);
     loff = (uint32_t)p * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(r))) * 16);
+  } else if (kMode == kPrecise) {
+    const int r = 8 * (wave & 3) + (lane >> 3);
+    const int p = row0 + min(r, rows - 1);
+    loff = (uint32_t)p * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
   }
 #pragma unroll
   for (int q = 0; q < 2; q++) {
@@ -844,27 +879,31 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
     const uint8_t* hbase = reinterpret_cast<const uint8_t*>(ch.hi) + (size_t)k * 128;
 #pragma unroll
     for (int q = 0; q < 2; q++) dma_lds16_s(hoff[q], hbase, st + (16 * wave + 8 * q) * 128);
-    if (kTwo) dma_lds16_s(loff, ch.lo + (size_t)k * 64, st + kB2Hi + 16 * wave * 64);
+    if (kMode == kTwoTerms) dma_lds16_s(loff, ch.lo + (size_t)k * 64, st + kB2Hi + 16 * wave * 64);
+    if (kMode == kPrecise)
+      dma_lds16_s(loff, reinterpret_cast<const uint8_t*>(ch.lo16) + (size_t)k * 128, st + kB2Hi + 8 * (wave & 3) * 128);
 #pragma unroll
     for (int q = 0; q < 2; q++) dma_lds16_s(woff[q], wbase + (size_t)k * 64, st + kB2Hi + kB2Lo + (32 * wave + 16 * q) * 64);
     dma_lds4_s(soff, ch.scale + k / 2, st + kB2Hi + kB2Lo + kB2W + (wave & 1) * 256);
   };
-  // operand read offsets: hi chunks 2kg + t of row lr (bg_key), lo / W2 chunk kg of row lr (bg_key4)
+  // operand read offsets: hi (and f16 lo) chunks 2kg + t of row lr (bg_key), e4m3 lo / W2 chunk kg
+  // of row lr (bg_key4)
   const int rh0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
   const int rh1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
   const int rq = lr * 64 + ((kg ^ bg_key4(lr)) * 16);
 
   MOEFP8_WAIT_VMCNT(0);
   for (int d = 0; d < kB2Stages - 1; d++) issue(d);
-  v4f acc[4][4];
+  v4f acc[NT][4];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < NT; i++)
 #pragma unroll
     for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < KS; j++) {
-    static_assert(kB2Stages == 3, "one stage in flight past the current one");
-    if (kTwo) MOEFP8_WAIT_VMCNT(6);
-    else MOEFP8_WAIT_VMCNT(5);
+    // one stage in flight past the current one: 5 (one term) or 6 operations per wavefront
+    static_assert(kB2Stages == 3, "wait count");
+    if (kMode == kOneTerm) MOEFP8_WAIT_VMCNT(5);
+    else MOEFP8_WAIT_VMCNT(6);
     barrier_lds();
     const uint8_t* st = ring + (j % kB2Stages) * kB2Stage;
     v8h b16[4][2];
@@ -874,21 +913,26 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
               b16[n][1]);
     const float sw = sw2_s[(j / 2) * 2 + (wn >> 1)];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int t = 4 * wm + i;
+    for (int i = 0; i < NT; i++) {
+      const int t = kMode == kPrecise ? wm : 4 * wm + i;
       const uint8_t* ht = st + t * 16 * 128;
       const v8h a0 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh0));
       const v8h a1 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh1));
       v8h l0 = {}, l1 = {};
-      if constexpr (kTwo)
+      if constexpr (kMode == kTwoTerms)
         widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + t * 16 * 64 + rq), 1.0f / kLoScale, l0, l1);
+      if constexpr (kMode == kPrecise) {
+        const uint8_t* lt = st + kB2Hi + t * 16 * 128;
+        l0 = as_v8h(*reinterpret_cast<const v4i*>(lt + rh0));
+        l1 = as_v8h(*reinterpret_cast<const v4i*>(lt + rh1));
+      }
       const float4 sa = *reinterpret_cast<const float4*>(st + kB2Hi + kB2Lo + kB2W + (16 * t + 4 * kg) * 4);
       const float4 sc = {sa.x * sw, sa.y * sw, sa.z * sw, sa.w * sw};
 #pragma unroll
       for (int n = 0; n < 4; n++) {
         v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b16[n][0], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b16[n][1], p, 0, 0, 0);
-        if constexpr (kTwo) {
+        if constexpr (kMode != kOneTerm) {
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, b16[n][0], p, 0, 0, 0);
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, b16[n][1], p, 0, 0, 0);
         }
@@ -902,10 +946,11 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
   }
   MOEFP8_WAIT_VMCNT(0);
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
+  for (int i = 0; i < NT; i++) {
+    const int t = kMode == kPrecise ? wm : 4 * wm + i;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const int row = 16 * (4 * wm + i) + 4 * kg + r;
+      const int row = 16 * t + 4 * kg + r;
       if (row < rows) {
         const int p = row0 + row;
         const float w = pl.perm_w[p];
@@ -916,12 +961,13 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
   }
 }
 
+// Units (m-block, 256 output columns) over the whole block table.
 __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Plan pl, CHalf8 ch,
                                                                  float* __restrict__ obuf) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kB2Stages * kB2Stage];
   __shared__ float sw2_s[2 * kBigMaxKB];
   const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock, HC = H / kB2Cols;
-  const int n_units = pl.info[7] * HC;
+  const int n_units = pl.info[5] * HC;
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
     const int mb = u / HC, hc = u % HC;
@@ -935,8 +981,12 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
       if (t < 2 * KB) sw2_s[t] = pb.s2[((size_t)e * HB + 2 * hc + (t & 1)) * KB + (t >> 1)];
     }
     __syncthreads();
-    if (flags & kFlagTwoTermC) gemm2_big_unit<true>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
-    else gemm2_big_unit<false>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+    if (flags & kFlagExactProducts)
+      gemm2_big_unit<kPrecise>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+    else if (flags & kFlagTwoTermC)
+      gemm2_big_unit<kTwoTerms>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+    else
+      gemm2_big_unit<kOneTerm>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
   }
 }
 

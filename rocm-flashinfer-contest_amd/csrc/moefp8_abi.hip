@@ -341,15 +341,13 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   launch_permute_large(pa, s);
   mark(2);
   if (large_big(T, H, I)) {
-    launch_gemm1_big(pb, pl, ch, (int)(L.max_blocks_a * (I / kBlock)), s);
-    launch_gemm1_large(pb, pl, ch, kExactRows / 16, (int)((L.max_blocks - L.max_blocks_a) * (I / kBlock)), 1, s);
+    launch_gemm1_big(pb, pl, ch, (int)(L.max_blocks * (I / kBlock)), s);
   } else {
     launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks * (I / kBlock)), 0, s);
   }
   mark(3);
   if (large_big(T, H, I)) {
-    launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks_a * (H / 256)), s);
-    launch_gemm2_large(pb, pl, ch, obuf, kExactRows / 16, (int)((L.max_blocks - L.max_blocks_a) * (H / kBlock)), 1, s);
+    launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks * (H / 256)), s);
   } else {
     launch_gemm2_large(pb, pl, ch, obuf, large_mt(T), (int)(L.max_blocks * (H / kBlock)), 0, s);
   }

@@ -116,7 +116,8 @@ int large_grid();
 // [info[7], info[2]) (from_exact = 1), 16 * mt rows per block
 void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units, int from_exact,
                         hipStream_t stream);
-// GEMM1 over the kBigRows-row class 0/1 blocks [0, info[7]), one workgroup per CU
+// GEMM1 over the whole table (kBigRows-row class 0/1 blocks, 32-row exact-product blocks), one
+// workgroup per CU
 constexpr int kBigRows = 128;
 constexpr int kBigMaxKB = 64;   // H <= 8192
 void launch_gemm1_big(const Problem& pb, const Plan& pl, const CHalf8& ch, int max_units, hipStream_t stream);
@@ -124,7 +125,7 @@ void launch_gemm1_big(const Problem& pb, const Plan& pl, const CHalf8& ch, int m
 // [info[7], info[5]) (from_exact = 1), blocks taken 16 * mt rows at a time
 void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
                         int from_exact, hipStream_t stream);
-// GEMM2 over the kBigRows-row class 0/1 blocks [0, info[7]), 256 output columns per unit
+// GEMM2 over the whole table, 256 output columns per unit
 void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int max_units,
                       hipStream_t stream);
 
