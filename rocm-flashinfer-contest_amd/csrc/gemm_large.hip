@@ -348,7 +348,7 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, 
 
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
     const int mb = mb_first + u / NCB, cb = u % NCB;
-    const int4 blk = pl.mblocks[mb];
+    const int4 blk = pl.mblocks1[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
     const int mvalid = (rows + 15) / 16;
     if (!(flags & kFlagExactProducts)) {
@@ -544,7 +544,7 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
         const _Float16 hi = (_Float16)v;
         ch.hi[p * I + col] = hi;
         if constexpr (kExact) ch.lo16[p * I + col] = (_Float16)(v - (float)hi);
-        else if (two)
+        else if (two)   // GEMM2's two-term blocks (class 1 rows) read it
           ch.lo[p * I + col] = (uint8_t)f32_to_e4m3(fminf(fmaxf((v - (float)hi) * kLoScale, -448.0f), 448.0f));
       }
       if (wn == 0 && lr == 0) ch.scale[p * NCB + cb] = scale;
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Pl
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
     const int mb = u / NCB, cb = u % NCB;
-    const int4 blk = pl.mblocks[mb];
+    const int4 blk = pl.mblocks1[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
     // the previous unit's readers are done with the ring, amax_s and sw_s
     __syncthreads();
@@ -755,21 +755,19 @@ __device__ __forceinline__ void gemm2_large_store(const Plan& pl, float* __restr
   }
 }
 
-// Units (m-block, 128 output columns) over blocks [first, info[5]) of the table, first = 0 or
-// info[7] (the exact-product blocks after the class 0/1 blocks that the 128-row kernel takes); a
-// block taller than 16 MT rows is taken 16 MT rows at a time.
+// Units (m-block, 128 output columns) over GEMM2's blocks; a block taller than 16 MT rows is taken
+// 16 MT rows at a time.
 template <int MT>
 __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, Plan pl, CHalf8 ch,
-                                                                     float* __restrict__ obuf, int from_exact) {
+                                                                     float* __restrict__ obuf) {
   using L = G2L<MT>;
   constexpr int NP = MT / 2;
   __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
   const int H = pb.H, HB = H / kBlock;
-  const int mb_first = from_exact ? pl.info[7] : 0;
-  const int n_units = (pl.info[5] - mb_first) * HB;
+  const int n_units = pl.info[5] * HB;
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-    const int mb = mb_first + u / HB, hb = u % HB;
-    const int4 blk = pl.mblocks[mb];
+    const int mb = u / HB, hb = u % HB;
+    const int4 blk = pl.mblocks2[mb];
     const int e = uniform(blk.x), flags = uniform(blk.w);
     for (int s0 = 0; s0 < blk.z; s0 += 16 * MT) {
       const int row0 = uniform(blk.y + s0), rows = uniform(min(16 * MT, blk.z - s0));
@@ -971,7 +969,7 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
     const int mb = u / HC, hc = u % HC;
-    const int4 blk = pl.mblocks[mb];
+    const int4 blk = pl.mblocks2[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
     // the previous unit's readers are done with the ring and sw2_s
     __syncthreads();
@@ -1016,17 +1014,15 @@ void launch_gemm1_big(const Problem& pb, const Plan& pl, const CHalf8& ch, int m
 }
 
 void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
-                        int from_exact, hipStream_t stream) {
+                        hipStream_t stream) {
   const int grid = max_units < large_grid() ? max_units : large_grid();
   if (grid <= 0) return;
   switch (mt) {
     case 2:
-      hipLaunchKernelGGL(gemm2_large_kernel<2>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, obuf,
-                         from_exact);
+      hipLaunchKernelGGL(gemm2_large_kernel<2>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, obuf);
       break;
     default:
-      hipLaunchKernelGGL(gemm2_large_kernel<4>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, obuf,
-                         from_exact);
+      hipLaunchKernelGGL(gemm2_large_kernel<4>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, obuf);
       break;
   }
 }

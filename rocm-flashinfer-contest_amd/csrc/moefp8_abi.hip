@@ -37,9 +37,9 @@ int large_rows_b(int64_t T, int H, int I) { return large_big(T, H, I) ? kExactRo
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
   size_t tok_a2, esig, perm_exact, mtiles, c16, c16_scale, gbuf, obuf;
-  size_t canon_token, bcnt, ccnt, mblocks, c_hi, c_lo, c_lo16, c_scale;
+  size_t canon_token, bcnt, ccnt, mblocks1, mblocks2, c_hi, c_lo, c_lo16, c_scale;
   size_t total;
-  int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks_a, max_blocks;
+  int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks1, max_blocks2;
   int nblk;
 };
 
@@ -86,12 +86,16 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.rows_cap = pmax;
   L.nblk = permute_large_blocks(T);
   const int ra = large_rows_a(T, H, I), rb = large_rows_b(T, H, I);
-  L.max_blocks_a = (pmax + ra - 1) / ra + 2 * E_local;   // class 0 and class 1 blocks per expert
-  L.max_blocks = L.max_blocks_a + (pmax + rb - 1) / rb + E_local;
+  // blocks per expert: GEMM1 ceil(class 0+1 rows / ra) + ceil(class 2 rows / rb); GEMM2 has the
+  // class 0 and class 1 rows in separate blocks (one more partial block per expert)
+  const int64_t exact_blocks = (pmax + rb - 1) / rb + E_local;
+  L.max_blocks1 = (pmax + ra - 1) / ra + E_local + exact_blocks;
+  L.max_blocks2 = (pmax + ra - 1) / ra + 2 * E_local + exact_blocks;
   L.canon_token = take((size_t)pmax * 4);
   L.bcnt = take((size_t)L.nblk * E_local * 3 * 4);
   L.ccnt = take((size_t)L.nblk * E_local * 4);
-  L.mblocks = take((size_t)L.max_blocks * 16);
+  L.mblocks1 = take((size_t)L.max_blocks1 * 16);
+  L.mblocks2 = take((size_t)L.max_blocks2 * 16);
   L.c_hi = take((size_t)pmax * I * 2);
   L.c_lo = take((size_t)pmax * I);
   L.c_lo16 = take((size_t)pmax * I * 2);
@@ -248,7 +252,8 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pl.info = reinterpret_cast<int*>(ws + L.info);
   pl.exact = ws + L.perm_exact;
   pl.mtiles = nullptr;
-  pl.mblocks = nullptr;
+  pl.mblocks1 = nullptr;
+  pl.mblocks2 = nullptr;
   pl.canon_token = pl.perm_token;
   float* tok_a2 = reinterpret_cast<float*>(ws + L.tok_a2);
   float* esig = reinterpret_cast<float*>(ws + L.esig);
@@ -323,11 +328,13 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pa.perm_w = const_cast<float*>(pl.perm_w);
   pa.canon_token = reinterpret_cast<int*>(ws + L.canon_token);
   pa.tok_slot = const_cast<int*>(pl.tok_slot);
-  pa.mblocks = reinterpret_cast<int4*>(ws + L.mblocks);
+  pa.mblocks1 = reinterpret_cast<int4*>(ws + L.mblocks1);
+  pa.mblocks2 = reinterpret_cast<int4*>(ws + L.mblocks2);
   pa.rows_a = large_rows_a(T, H, I);
   pa.rows_b = large_rows_b(T, H, I);
   pl.canon_token = pa.canon_token;
-  pl.mblocks = pa.mblocks;
+  pl.mblocks1 = pa.mblocks1;
+  pl.mblocks2 = pa.mblocks2;
   CHalf8 ch;
   ch.hi = reinterpret_cast<_Float16*>(ws + L.c_hi);
   ch.lo = ws + L.c_lo;
@@ -341,15 +348,15 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   launch_permute_large(pa, s);
   mark(2);
   if (large_big(T, H, I)) {
-    launch_gemm1_big(pb, pl, ch, (int)(L.max_blocks * (I / kBlock)), s);
+    launch_gemm1_big(pb, pl, ch, (int)(L.max_blocks1 * (I / kBlock)), s);
   } else {
-    launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks * (I / kBlock)), 0, s);
+    launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks1 * (I / kBlock)), 0, s);
   }
   mark(3);
   if (large_big(T, H, I)) {
-    launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks * (H / 256)), s);
+    launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks2 * (H / 256)), s);
   } else {
-    launch_gemm2_large(pb, pl, ch, obuf, large_mt(T), (int)(L.max_blocks * (H / kBlock)), 0, s);
+    launch_gemm2_large(pb, pl, ch, obuf, large_mt(T), (int)(L.max_blocks2 * (H / kBlock)), s);
   }
   mark(4);
   launch_combine(pl, obuf, a->output, (int)T, H, s);

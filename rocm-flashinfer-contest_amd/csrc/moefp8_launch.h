@@ -44,13 +44,15 @@ struct Plan {
   const int* tok_slot;        // [T * 8]
   const int* active;          // [E_local]
   const int* mtile_offsets;   // [E_local + 1]
-  const int* info;            // {P, n_active, m-blocks|m-tiles, S1, S2, GEMM2 m-blocks, m-tiles, large T:
-                              //  class 0/1 m-blocks}
+  const int* info;            // {P, n_active, GEMM1 m-blocks|m-tiles, S1, S2, GEMM2 m-blocks, m-tiles,
+                              //  large T: GEMM1 blocks before the exact-product ones}
   const uint8_t* exact;       // small T: [Pmax] per-pair flags (kFlagExactProducts, kFlagTwoTermC)
   const int4* mtiles;         // small T: per m-tile {expert, first pair, rows, OR of pair flags}
-  const int4* mblocks;        // large T: m-blocks {expert, first row, rows, OR of pair flags}, both GEMMs;
-                              // blocks of the expert's class 0/1 rows first (info[7] of them), then
-                              // blocks of its exact-product rows
+  const int4* mblocks1;       // large T, GEMM1: m-blocks {expert, first row, rows, flags} over each
+                              // expert's class 0 and 1 rows together (info[7] of them), then over its
+                              // exact-product rows; info[2] blocks in all
+  const int4* mblocks2;       // large T, GEMM2: the same with class 0 and class 1 rows in separate
+                              // blocks (one precision mode per block); info[5] blocks in all
   const int* canon_token;     // token of each pair in canonical (expert, token) order
 };
 
@@ -97,7 +99,8 @@ struct LargePermArgs {
   float* perm_w;        // [Pmax]
   int* canon_token;     // [Pmax] canonical order
   int* tok_slot;        // [T * 8] internal rows of each token's pairs, ascending expert
-  int4* mblocks;        // [max blocks] {expert, first row, rows, flags}
+  int4* mblocks1;       // GEMM1 m-blocks {expert, first row, rows, flags}
+  int4* mblocks2;       // GEMM2 m-blocks
   int rows_a;           // block height over an expert's class 0 and 1 rows
   int rows_b;           // block height over its class 2 (exact-product) rows
 };
@@ -112,7 +115,7 @@ struct CHalf8 {
   float* scale;     // [Pmax][I/128]
 };
 int large_grid();
-// GEMM1 over blocks [0, info[2]) (from_exact = 0) or over the exact-product blocks
+// GEMM1 over its blocks [0, info[2]) (from_exact = 0) or over its exact-product blocks
 // [info[7], info[2]) (from_exact = 1), 16 * mt rows per block
 void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units, int from_exact,
                         hipStream_t stream);
@@ -121,10 +124,9 @@ void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int
 constexpr int kBigRows = 128;
 constexpr int kBigMaxKB = 64;   // H <= 8192
 void launch_gemm1_big(const Problem& pb, const Plan& pl, const CHalf8& ch, int max_units, hipStream_t stream);
-// GEMM2 over blocks [0, info[5]) (from_exact = 0) or over the exact-product blocks
-// [info[7], info[5]) (from_exact = 1), blocks taken 16 * mt rows at a time
+// GEMM2 over its blocks [0, info[5]), blocks taken 16 * mt rows at a time
 void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
-                        int from_exact, hipStream_t stream);
+                        hipStream_t stream);
 // GEMM2 over the whole table, 256 output columns per unit
 void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int max_units,
                       hipStream_t stream);
