@@ -152,10 +152,56 @@ def measure(wl, weights, steps, warmup, flush):
     else:
         ach = k_flops / (k_us * 1e-6) / 1e12
         roof = dict(bound="mfma", achieved=ach, peak=FP8_PEAK / 1e12, unit="TFLOP/s", frac=ach / (FP8_PEAK / 1e12))
-    roof.update(kernel=dom, kernel_us=k_us, algorithmic_bytes=k_bytes, algorithmic_flops=k_flops, traffic=None)
+    roof.update(kernel=dom, kernel_us=k_us, algorithmic_bytes=k_bytes, algorithmic_flops=k_flops,
+                traffic=measured_traffic(dom, wl.name))
     res["roofline"] = roof
     del runner
     return res
+
+
+# The library's kernel names per bench stage ("gemm1" / "gemm2"), by path: decode (T <= 64), and
+# the 128-row grouped GEMMs of the large path.
+STAGE_KERNELS = {("gemm1", "decode"): "gemm1_decode_kernel", ("gemm2", "decode"): "gemm2_decode_kernel",
+                 ("gemm1", "large"): "gemm1_big_kernel", ("gemm2", "large"): "gemm2_big_kernel"}
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.txt"
+
+
+def measured_traffic(stage, workload):
+    """HBM bytes per launch of the stage's kernel on this workload, from the rocprofv3 FETCH_SIZE
+    and WRITE_SIZE readings recorded in profiles/hbm_traffic.txt, each divided by what the same
+    counter reads per byte for a plain device copy; None when not recorded."""
+    path = "decode" if workload.startswith(("decode", "plumbing")) else "large"
+    kernel = STAGE_KERNELS.get((stage, path))
+    if kernel is None or not TRAFFIC_FILE.exists():
+        return None
+    rec, cal = None, None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("#") or "=" not in line:
+            continue
+        kv = dict(x.split("=", 1) for x in line.split())
+        if kv.get("kernel") == "copy":
+            cal = kv
+        elif kv.get("kernel") == kernel and kv.get("workload") == workload:
+            rec = kv
+    if rec is None or cal is None:
+        return None
+    fetch_per_byte = float(cal["fetch_kib"]) * 1024 / float(cal["bytes"])
+    write_per_byte = float(cal["write_kib"]) * 1024 / float(cal["bytes"])
+    return round(float(rec["fetch_kib"]) * 1024 / fetch_per_byte + float(rec["write_kib"]) * 1024 / write_per_byte)
+
+
+def copy_calibration():
+    """A plain 256 MiB device-to-device copy, three times: the reference kernel for scaling the
+    FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"# copy calibration: {n} bytes per copy", file=sys.stderr)
+    return 0
 
 
 def cpu_baseline(wl, weights_cpu, threads):
@@ -183,7 +229,11 @@ def main():
     ap.add_argument("--secondary", default="large_t8192")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 256 MiB device copy (counter calibration under rocprofv3)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the operator runs all 32 local experts of one expert-parallel rank on a "
               f"single MI355X; --gpus {args.gpus} is not supported", file=sys.stderr)

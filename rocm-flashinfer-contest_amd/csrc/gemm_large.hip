@@ -334,20 +334,18 @@ __device__ __forceinline__ void gemm1_large_store(const Plan& pl, const CHalf8& 
   __syncthreads();
 }
 
-// Units (m-block, 128 output columns) over blocks [first, info[2]) of the table; first = 0, or
-// info[7] (the exact-product blocks after the class 0/1 blocks that the 128-row kernel takes).
+// Units (m-block, 128 output columns) over GEMM1's blocks.
 template <int MT>
-__global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, Plan pl, CHalf8 ch, int from_exact) {
+__global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, Plan pl, CHalf8 ch) {
   using L = G1L<MT>;
   static_assert(MT % 2 == 0, "two activation DMAs per m-tile");
   __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
   __shared__ float amax_s[kLgWaves][16 * MT];
   const int I = pb.I, NCB = I / kBlock;
-  const int mb_first = from_exact ? pl.info[7] : 0;
-  const int n_units = (pl.info[2] - mb_first) * NCB;
+  const int n_units = pl.info[2] * NCB;
 
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-    const int mb = mb_first + u / NCB, cb = u % NCB;
+    const int mb = u / NCB, cb = u % NCB;
     const int4 blk = pl.mblocks1[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
     const int mvalid = (rows + 15) / 16;
@@ -552,8 +550,8 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
   }
 }
 
-// Units (m-block, 128 C columns) over the whole block table: the 128-row class 0/1 blocks, then
-// the exact-product blocks.
+// Units (m-block, 128 C columns) over GEMM1's blocks (128-row class 0/1 blocks and 32-row
+// exact-product blocks).
 __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Plan pl, CHalf8 ch) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kBgStages * kBgStage];
   __shared__ __attribute__((aligned(16))) float2 sw_s[kBigMaxKB];
@@ -959,7 +957,7 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
   }
 }
 
-// Units (m-block, 256 output columns) over the whole block table.
+// Units (m-block, 256 output columns) over GEMM2's blocks.
 __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Plan pl, CHalf8 ch,
                                                                  float* __restrict__ obuf) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kB2Stages * kB2Stage];
@@ -991,16 +989,16 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
 // ------------------------------------------------------------------------------------------ launch
 int large_grid() { return num_compute_units() * 2; }
 
-void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units, int from_exact,
+void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units,
                         hipStream_t stream) {
   const int grid = max_units < large_grid() ? max_units : large_grid();
   if (grid <= 0) return;
   switch (mt) {
     case 2:
-      hipLaunchKernelGGL(gemm1_large_kernel<2>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, from_exact);
+      hipLaunchKernelGGL(gemm1_large_kernel<2>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch);
       break;
     default:
-      hipLaunchKernelGGL(gemm1_large_kernel<4>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch, from_exact);
+      hipLaunchKernelGGL(gemm1_large_kernel<4>, dim3(grid), dim3(kLgThreads), 0, stream, pb, pl, ch);
       break;
   }
 }

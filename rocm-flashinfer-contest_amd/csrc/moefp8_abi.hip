@@ -350,7 +350,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   if (large_big(T, H, I)) {
     launch_gemm1_big(pb, pl, ch, (int)(L.max_blocks1 * (I / kBlock)), s);
   } else {
-    launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks1 * (I / kBlock)), 0, s);
+    launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks1 * (I / kBlock)), s);
   }
   mark(3);
   if (large_big(T, H, I)) {

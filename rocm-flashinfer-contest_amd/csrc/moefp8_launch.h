@@ -44,13 +44,12 @@ struct Plan {
   const int* tok_slot;        // [T * 8]
   const int* active;          // [E_local]
   const int* mtile_offsets;   // [E_local + 1]
-  const int* info;            // {P, n_active, GEMM1 m-blocks|m-tiles, S1, S2, GEMM2 m-blocks, m-tiles,
-                              //  large T: GEMM1 blocks before the exact-product ones}
+  const int* info;            // {P, n_active, GEMM1 m-blocks|m-tiles, S1, S2, GEMM2 m-blocks, m-tiles}
   const uint8_t* exact;       // small T: [Pmax] per-pair flags (kFlagExactProducts, kFlagTwoTermC)
   const int4* mtiles;         // small T: per m-tile {expert, first pair, rows, OR of pair flags}
-  const int4* mblocks1;       // large T, GEMM1: m-blocks {expert, first row, rows, flags} over each
-                              // expert's class 0 and 1 rows together (info[7] of them), then over its
-                              // exact-product rows; info[2] blocks in all
+  const int4* mblocks1;       // large T, GEMM1: m-blocks {expert, first row, rows, flags}, expert by
+                              // expert: its class 0 and 1 rows together, then its exact-product rows;
+                              // info[2] blocks in all
   const int4* mblocks2;       // large T, GEMM2: the same with class 0 and class 1 rows in separate
                               // blocks (one precision mode per block); info[5] blocks in all
   const int* canon_token;     // token of each pair in canonical (expert, token) order
@@ -115,9 +114,8 @@ struct CHalf8 {
   float* scale;     // [Pmax][I/128]
 };
 int large_grid();
-// GEMM1 over its blocks [0, info[2]) (from_exact = 0) or over its exact-product blocks
-// [info[7], info[2]) (from_exact = 1), 16 * mt rows per block
-void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units, int from_exact,
+// GEMM1 over its blocks [0, info[2]), 16 * mt rows per block
+void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int mt, int max_units,
                         hipStream_t stream);
 // GEMM1 over the whole table (kBigRows-row class 0/1 blocks, 32-row exact-product blocks), one
 // workgroup per CU
