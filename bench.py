@@ -163,26 +163,27 @@ def measure(wl, weights, steps, warmup, flush):
 # the 128-row grouped GEMMs of the large path.
 STAGE_KERNELS = {("gemm1", "decode"): "gemm1_decode_kernel", ("gemm2", "decode"): "gemm2_decode_kernel",
                  ("gemm1", "large"): "gemm1_big_kernel", ("gemm2", "large"): "gemm2_big_kernel"}
-TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.txt"
+PROFILES = ROOT / "profiles"
 
 
 def measured_traffic(stage, workload):
     """HBM bytes per launch of the stage's kernel on this workload, from the rocprofv3 FETCH_SIZE
-    and WRITE_SIZE readings recorded in profiles/hbm_traffic.txt, each divided by what the same
-    counter reads per byte for a plain device copy; None when not recorded."""
+    and WRITE_SIZE readings recorded in profiles/traffic_<kernel>_<workload>.txt, each divided by
+    what the same counter reads per byte for a plain device copy (profiles/traffic_copy.txt);
+    None when not recorded."""
     path = "decode" if workload.startswith(("decode", "plumbing")) else "large"
     kernel = STAGE_KERNELS.get((stage, path))
-    if kernel is None or not TRAFFIC_FILE.exists():
+
+    def record(name):
+        f = PROFILES / f"traffic_{name}.txt"
+        if not f.exists():
+            return None
+        for line in f.read_text().splitlines():
+            if line.startswith("record "):
+                return dict(x.split("=", 1) for x in line.split()[1:])
         return None
-    rec, cal = None, None
-    for line in TRAFFIC_FILE.read_text().splitlines():
-        if line.startswith("#") or "=" not in line:
-            continue
-        kv = dict(x.split("=", 1) for x in line.split())
-        if kv.get("kernel") == "copy":
-            cal = kv
-        elif kv.get("kernel") == kernel and kv.get("workload") == workload:
-            rec = kv
+
+    rec, cal = (record(f"{kernel}_{workload}") if kernel else None), record("copy")
     if rec is None or cal is None:
         return None
     fetch_per_byte = float(cal["fetch_kib"]) * 1024 / float(cal["bytes"])

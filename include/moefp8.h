@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOEFP8_ABI_VERSION 1
+#define MOEFP8_ABI_VERSION 2
 
 /* Operator constants (solutions/moe_fp8/main.py:22-29). */
 #define MOEFP8_E_GLOBAL 256
@@ -92,12 +92,13 @@ typedef struct moefp8_args {
   int32_t* permuted_tokens;
   /* optional, may be NULL: array of MOEFP8_NUM_STAGE_EVENTS hipEvent_t created by the
    * caller.  Event i is recorded on `stream` before stage i (route, permute, GEMM1,
-   * GEMM2, combine) and the last one after the combine, so stage i's device time is
+   * activation, GEMM2, combine; the activation stage is empty where GEMM1 applies SwiGLU
+   * itself) and the last one after the combine, so stage i's device time is
    * hipEventElapsedTime(ev[i], ev[i+1]).  Used for live per-kernel timing. */
   void* stage_events;
 } moefp8_args;
 
-#define MOEFP8_NUM_STAGE_EVENTS 6
+#define MOEFP8_NUM_STAGE_EVENTS 7
 
 /* ABI version of the loaded library (MOEFP8_ABI_VERSION of its build). */
 int moefp8_abi_version(void);

@@ -299,12 +299,13 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
     ch.lo = ch.hi + L.c_plane;
     ch.scale = reinterpret_cast<float*>(ws + L.c16_scale);
     launch_gemm1_decode(pb, pl, gbuf, s);
-    launch_activation_decode(pb, pl, gbuf, ch, (int)L.pmax, s);
     mark(3);
-    launch_gemm2_decode(pb, pl, ch, obuf, s);
+    launch_activation_decode(pb, pl, gbuf, ch, (int)L.pmax, s);
     mark(4);
-    launch_combine(pl, obuf, a->output, (int)T, H, s);
+    launch_gemm2_decode(pb, pl, ch, obuf, s);
     mark(5);
+    launch_combine(pl, obuf, a->output, (int)T, H, s);
+    mark(6);
     return finish(a, L, topk_ids, topk_w, pl, s);
   }
   // large T: routing, permutation (3 launches), GEMM1 (+SwiGLU, C split), GEMM2, combine
@@ -353,14 +354,15 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
     launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks1 * (I / kBlock)), s);
   }
   mark(3);
+  mark(4);   // SwiGLU is GEMM1's epilogue here: empty activation stage
   if (large_big(T, H, I)) {
     launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks2 * (H / 256)), s);
   } else {
     launch_gemm2_large(pb, pl, ch, obuf, large_mt(T), (int)(L.max_blocks2 * (H / kBlock)), s);
   }
-  mark(4);
-  launch_combine(pl, obuf, a->output, (int)T, H, s);
   mark(5);
+  launch_combine(pl, obuf, a->output, (int)T, H, s);
+  mark(6);
   return finish(a, L, topk_ids, topk_w, pl, s);
 }
 

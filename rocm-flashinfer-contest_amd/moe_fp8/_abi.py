@@ -12,7 +12,7 @@ from pathlib import Path
 LIB_NAME = "libmoefp8.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -61,8 +61,8 @@ class MoeFp8Args(ctypes.Structure):
     ]
 
 
-NUM_STAGE_EVENTS = 6
-STAGES = ("route", "permute", "gemm1", "gemm2", "combine")
+NUM_STAGE_EVENTS = 7
+STAGES = ("route", "permute", "gemm1", "activation", "gemm2", "combine")
 
 
 class MoeFp8Error(RuntimeError):
