@@ -30,7 +30,10 @@
 namespace moefp8 {
 
 constexpr int kDecBlockWaves = 4;            // wavefronts per workgroup = column groups per unit
-constexpr int kDecBlocksPerCU = 5;           // resident workgroups per CU (<= 96 VGPRs)
+constexpr int kDec1BlocksPerCU = 5;          // GEMM1 resident workgroups per CU (<= 96 VGPRs)
+constexpr int kDec2BlocksPerCU = 4;          // GEMM2: its f16 operands need ~100 VGPRs (<= 128); at
+                                             // 5 per CU it spills, and the scratch traffic costs
+                                             // ~20% of its time (measured)
 constexpr int kDecDepth = 3;                 // K-blocks in flight per wavefront (register ring)
 
 __device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
@@ -74,7 +77,7 @@ struct alignas(16) G2Stage {
 // registers, then loads its pieces of step j + kDecDepth.  A stage is rewritten two
 // steps after it was read, i.e. after the barrier that follows every wavefront's read.
 
-__global__ __launch_bounds__(64 * kDecBlockWaves, kDecBlocksPerCU) void gemm1_decode_kernel(Problem pb, Plan pl,
+__global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_decode_kernel(Problem pb, Plan pl,
                                                                                              float* __restrict__ gbuf) {
   __shared__ G1Stage ring[2];
   const int n_mt = pl.info[2], S = pl.info[3];
@@ -212,7 +215,7 @@ __global__ __launch_bounds__(256) void activation_decode_kernel(int I, Plan pl, 
   if (lane == 0) ch.scale[(size_t)p * CB + cb] = scale;
 }
 
-__global__ __launch_bounds__(64 * kDecBlockWaves, kDecBlocksPerCU) void gemm2_decode_kernel(Problem pb, Plan pl,
+__global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_decode_kernel(Problem pb, Plan pl,
                                                                                              CHalf ch,
                                                                                              float* __restrict__ obuf) {
   __shared__ G2Stage ring[2];
@@ -318,13 +321,14 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDecBlocksPerCU) void gemm2_de
   }
 }
 
-// Resident capacity of the 4-wave, <= 96-VGPR decode GEMMs, in workgroups, and the
-// number of 16-column groups one workgroup unit covers.
-int decode_grid() { return num_compute_units() * kDecBlocksPerCU; }
+// Resident capacity of the 4-wave decode GEMMs, in workgroups, and the number of
+// 16-column groups one workgroup unit covers.
+int decode_grid1() { return num_compute_units() * kDec1BlocksPerCU; }
+int decode_grid2() { return num_compute_units() * kDec2BlocksPerCU; }
 int decode_unit_groups() { return kDecBlockWaves; }
 
 void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, hipStream_t stream) {
-  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(decode_grid()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, gbuf);
+  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(decode_grid1()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, gbuf);
 }
 
 void launch_activation_decode(const Problem& pb, const Plan& pl, const float* gbuf, const CHalf& ch, int pmax,
@@ -335,7 +339,7 @@ void launch_activation_decode(const Problem& pb, const Plan& pl, const float* gb
 }
 
 void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, hipStream_t stream) {
-  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(decode_grid()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, ch,
+  hipLaunchKernelGGL(gemm2_decode_kernel, dim3(decode_grid2()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, ch,
                      obuf);
 }
 

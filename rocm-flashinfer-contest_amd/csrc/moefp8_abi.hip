@@ -278,9 +278,9 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
                    H, I, E_local, tok_a2, esig};
   if (T <= kDecodeMaxT) {
     // small T: routing (+ scale estimates), permutation, GEMM1, activation, GEMM2, combine
-    const int slots = decode_grid(), groups = decode_unit_groups();
-    const SplitPolicy sp = {slots, 2 * I / (16 * groups), H / kBlock, (int)L.rows_cap,
-                            slots, H / (16 * groups),     I / kBlock, (int)L.rows_cap};
+    const int groups = decode_unit_groups();
+    const SplitPolicy sp = {decode_grid1(), 2 * I / (16 * groups), H / kBlock, (int)L.rows_cap,
+                            decode_grid2(), H / (16 * groups),     I / kBlock, (int)L.rows_cap};
     pl.mtiles = reinterpret_cast<const int4*>(ws + L.mtiles);
     mark(0);
     launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,

@@ -71,7 +71,8 @@ struct CHalf {
   _Float16* lo;   // [Pmax][I]
   float* scale;   // [Pmax][I/128]
 };
-int decode_grid();
+int decode_grid1();
+int decode_grid2();
 int decode_unit_groups();
 void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, hipStream_t stream);
 void launch_activation_decode(const Problem& pb, const Plan& pl, const float* gbuf, const CHalf& ch, int pmax,
