@@ -92,8 +92,8 @@ typedef struct moefp8_args {
   int32_t* permuted_tokens;
   /* optional, may be NULL: array of MOEFP8_NUM_STAGE_EVENTS hipEvent_t created by the
    * caller.  Event i is recorded on `stream` before stage i (route, permute, GEMM1,
-   * activation, GEMM2, combine; the activation stage is empty where GEMM1 applies SwiGLU
-   * itself) and the last one after the combine, so stage i's device time is
+   * activation, GEMM2, combine; GEMM1 applies SwiGLU itself, so the activation stage is
+   * empty) and the last one after the combine, so stage i's device time is
    * hipEventElapsedTime(ev[i], ev[i+1]).  Used for live per-kernel timing. */
   void* stage_events;
 } moefp8_args;

@@ -16,8 +16,9 @@
 // still fits the grid, so a handful of active experts still spreads over every CU; the S
 // partial sums go to separate rows and the next stage adds them in ascending order.
 //
-// GEMM1       G1 partials = A_e W13_e^T over a K-slice                  (main.py:229-231)
-// activation  C = silu(sum_s G1[:, I:]) * sum_s G1[:, :I]              (main.py:232-233),
+// GEMM1       G1 partials = A_e W13_e^T over a K-slice                  (main.py:229-231);
+//             the last unit to finish a (m-tile, 128 C columns) group then forms
+//             C = silu(sum_s G1[:, I:]) * sum_s G1[:, :I]              (main.py:232-233),
 //             stored as f16 hi + lo with one fp32 scale per (pair, 128 columns)
 // GEMM2       O partials = routing weight * C W2_e^T over a K-slice   (main.py:234-241),
 //             exact products of C's f16 hi term (2^-11 relative) and W2 widened to f16
@@ -77,11 +78,77 @@ struct alignas(16) G2Stage {
 // registers, then loads its pieces of step j + kDecDepth.  A stage is rewritten two
 // steps after it was read, i.e. after the barrier that follows every wavefront's read.
 
+// Partial sums that another workgroup of the same launch reads (possibly on another XCD,
+// whose L2 is not coherent with this one's) are stored and loaded at device scope: the
+// stores write through to the device-coherent level and the loads read from it, so no
+// cache-wide fence is needed (a device-scope fence writes back and invalidates the whole
+// L2; one per unit multiplied GEMM1's time by 5, measured).
+__device__ __forceinline__ void store_shared_f32(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_shared_f32x2(const float* p) {
+  return __builtin_bit_cast(float2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT));
+}
+// Counts one more arrival at *counter once this workgroup's device-scope stores are
+// complete; true in every thread of the workgroup that arrived last of `expected`.
+__device__ __forceinline__ bool arrive_last(int* counter, int expected, int* flag_s) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *flag_s = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expected - 1;
+  __syncthreads();
+  return *flag_s;
+}
+
+// SwiGLU of pair p's C columns [128 cb, 128 cb + 128) by one wavefront: sums the GEMM1
+// partials of the S K-splits in split order, applies silu(gate) * up and writes C as two
+// f16 terms with one scale (max |C| -> 448).
+__device__ __forceinline__ void swiglu_block(int I, int S, int p, int cb, const float* __restrict__ gbuf,
+                                             const CHalf& ch) {
+  constexpr int kBatch = 8;   // partial loads issued together
+  const int CB = I / kBlock, I2 = 2 * I;
+  const int lane = lane_id();
+  const int c = cb * kBlock + 2 * lane;
+  float2 up = {0.f, 0.f}, gate = {0.f, 0.f};
+  for (int s0 = 0; s0 < S; s0 += kBatch) {
+    float2 u[kBatch], g[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; q++) {
+      const int s = min(s0 + q, S - 1);
+      const float* row = gbuf + ((size_t)p * S + s) * I2;
+      u[q] = load_shared_f32x2(row + c);
+      g[q] = load_shared_f32x2(row + I + c);
+    }
+#pragma unroll
+    for (int q = 0; q < kBatch; q++) {
+      if (s0 + q < S) {
+        up.x += u[q].x;
+        up.y += u[q].y;
+        gate.x += g[q].x;
+        gate.y += g[q].y;
+      }
+    }
+  }
+  const float c0 = silu_f32(gate.x) * up.x, c1 = silu_f32(gate.y) * up.y;
+  const float amax = wave_max_f32(fmaxf(fabsf(c0), fabsf(c1)));
+  float inv, scale;
+  split_scale(amax, inv, scale);
+  _Float16 h0, l0, h1, l1;
+  split_f16(c0, inv, h0, l0);
+  split_f16(c1, inv, h1, l1);
+  *reinterpret_cast<v2h*>(ch.hi + (size_t)p * I + c) = v2h{h0, h1};
+  *reinterpret_cast<v2h*>(ch.lo + (size_t)p * I + c) = v2h{l0, l1};
+  if (lane == 0) ch.scale[(size_t)p * CB + cb] = scale;
+}
+
 __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_decode_kernel(Problem pb, Plan pl,
-                                                                                             float* __restrict__ gbuf) {
+                                                                                             float* __restrict__ gbuf,
+                                                                                             CHalf ch) {
   __shared__ G1Stage ring[2];
+  __shared__ int last_s;
   const int n_mt = pl.info[2], S = pl.info[3];
-  const int H = pb.H, I2 = 2 * pb.I, T = pb.T;
+  const int H = pb.H, I = pb.I, I2 = 2 * pb.I, T = pb.T;
   const int KB = H / kBlock, NCB = I2 / (16 * kDecBlockWaves);
   const int n_units = n_mt * S * NCB;
   const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
@@ -106,15 +173,16 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
       // compiler's wait counting fall back to draining all of them.
       const uint8_t* asrc = pb.hidden + (size_t)tok * H + (size_t)kb0 * kBlock + (4 * (wave & 1) + kg) * 16;
       const float* ssrc = pb.hscale + (size_t)kb0 * T + tok;
+      // weight scale of K-block kb0 + l in lane l (n <= 64), read per step with readlane
+      const float swv = swp[min(lane, n - 1)];
       v8i B[kDecDepth];
       v4i AR[kDecDepth];
-      float SR[kDecDepth], SW[kDecDepth];
+      float SR[kDecDepth];
       auto load = [&](int d, int j) {
         const int jj = min(j, n - 1);
         B[d] = load_v8i(bp + (size_t)jj * kBlock);
         AR[d] = *reinterpret_cast<const v4i*>(asrc + (size_t)jj * kBlock);
         SR[d] = ssrc[(size_t)jj * T];
-        SW[d] = swp[jj];
       };
       auto step = [&](int d, int j) {
         G1Stage& st = ring[j & 1];
@@ -124,7 +192,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
         const v4i x = *reinterpret_cast<const v4i*>(st.a + ((2 * kg) * 16 + lr) * 16);
         const v4i y = *reinterpret_cast<const v4i*>(st.a + ((2 * kg + 1) * 16 + lr) * 16);
         const float4 sa = *reinterpret_cast<const float4*>(st.sa + 4 * kg);
-        const float sw = SW[d];
+        const float sw = readlane_f32(swv, j);
         const v4f p = mfma16x16x128(__builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7), B[d],
                                     v4f{0.f, 0.f, 0.f, 0.f});
         acc[0] += p[0] * (sa.x * sw);
@@ -177,42 +245,15 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int row = 4 * kg + r;
-      if (row < M) gbuf[((size_t)(row0 + row) * S + du.s) * I2 + cg * 16 + lr] = acc[r];
+      if (row < M) store_shared_f32(gbuf + ((size_t)(row0 + row) * S + du.s) * I2 + cg * 16 + lr, acc[r]);
     }
+    // C columns [128 j, 128 j + 128) of the m-tile need the partials of 4 S units: column
+    // blocks 2j, 2j + 1 ("up") and NCB/2 + 2j, NCB/2 + 2j + 1 ("gate"), S K-splits each.
+    // Every unit publishes its partials and counts itself in; the last one forms C.
+    const int j = (du.cb % (NCB / 2)) / 2;
+    if (arrive_last(pl.counters + du.g * (I / kBlock) + j, 4 * S, &last_s))
+      for (int r = wave; r < M; r += kDecBlockWaves) swiglu_block(I, S, row0 + r, j, gbuf, ch);
   }
-}
-
-// One wavefront per (pair p, 128-column block): sums the GEMM1 partials in split order,
-// applies SwiGLU and writes C as two f16 terms with one scale (max |C| -> 448).
-__global__ __launch_bounds__(256) void activation_decode_kernel(int I, Plan pl, const float* __restrict__ gbuf,
-                                                                CHalf ch) {
-  const int P = pl.info[0], S = pl.info[3];
-  const int CB = I / kBlock, I2 = 2 * I;
-  const int w = blockIdx.x * 4 + wave_index();
-  if (w >= P * CB) return;
-  const int p = w / CB, cb = w - p * CB;
-  const int lane = lane_id();
-  const int c = cb * kBlock + 2 * lane;
-  float2 up = {0.f, 0.f}, gate = {0.f, 0.f};
-  for (int s = 0; s < S; s++) {
-    const float* row = gbuf + ((size_t)p * S + s) * I2;
-    const float2 u = *reinterpret_cast<const float2*>(row + c);
-    const float2 g = *reinterpret_cast<const float2*>(row + I + c);
-    up.x += u.x;
-    up.y += u.y;
-    gate.x += g.x;
-    gate.y += g.y;
-  }
-  const float c0 = silu_f32(gate.x) * up.x, c1 = silu_f32(gate.y) * up.y;
-  const float amax = wave_max_f32(fmaxf(fabsf(c0), fabsf(c1)));
-  float inv, scale;
-  split_scale(amax, inv, scale);
-  _Float16 h0, l0, h1, l1;
-  split_f16(c0, inv, h0, l0);
-  split_f16(c1, inv, h1, l1);
-  *reinterpret_cast<v2h*>(ch.hi + (size_t)p * I + c) = v2h{h0, h1};
-  *reinterpret_cast<v2h*>(ch.lo + (size_t)p * I + c) = v2h{l0, l1};
-  if (lane == 0) ch.scale[(size_t)p * CB + cb] = scale;
 }
 
 __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_decode_kernel(Problem pb, Plan pl,
@@ -241,15 +282,15 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       // lanes < 16 the scale of row lane (all lanes load it: no loads under a branch)
       const _Float16* asrc = ch.hi + (size_t)prow * I + (size_t)kb0 * kBlock + (4 * wave + kg) * 8;
       const float* ssrc = ch.scale + (size_t)prow * KB + kb0;
+      const float swv = swp[min(lane, n - 1)];
       v8i B[kDecDepth];
       v4i AR[kDecDepth];
-      float SR[kDecDepth], SW[kDecDepth];
+      float SR[kDecDepth];
       auto load = [&](int d, int j) {
         const int jj = min(j, n - 1);
         B[d] = load_v8i(bp + (size_t)jj * kBlock);
         AR[d] = *reinterpret_cast<const v4i*>(asrc + (size_t)jj * kBlock);
         SR[d] = ssrc[jj];
-        SW[d] = swp[jj];
       };
       auto step = [&](int d, int j) {
         G2Stage& st = ring[j & 1];
@@ -260,7 +301,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
 #pragma unroll
         for (int t = 0; t < 4; t++) ah[t] = *reinterpret_cast<const v8h*>(st.a + ((4 * kg + t) * 16 + lr) * 8);
         const float4 sa = *reinterpret_cast<const float4*>(st.sa + 4 * kg);
-        const float sw = SW[d];
+        const float sw = readlane_f32(swv, j);
         v8h b16[4];
         widen_fp8_operand(B[d], b16);
         const v4f p = mfma_f16_block(ah, b16, v4f{0.f, 0.f, 0.f, 0.f});
@@ -327,15 +368,9 @@ int decode_grid1() { return num_compute_units() * kDec1BlocksPerCU; }
 int decode_grid2() { return num_compute_units() * kDec2BlocksPerCU; }
 int decode_unit_groups() { return kDecBlockWaves; }
 
-void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, hipStream_t stream) {
-  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(decode_grid1()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, gbuf);
-}
-
-void launch_activation_decode(const Problem& pb, const Plan& pl, const float* gbuf, const CHalf& ch, int pmax,
-                              hipStream_t stream) {
-  const int waves = pmax * (pb.I / kBlock);
-  if (waves <= 0) return;
-  hipLaunchKernelGGL(activation_decode_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, pb.I, pl, gbuf, ch);
+void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, const CHalf& ch, hipStream_t stream) {
+  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(decode_grid1()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, gbuf,
+                     ch);
 }
 
 void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, hipStream_t stream) {

@@ -34,7 +34,8 @@ void launch_route(const void* logits, int logits_dt, const void* bias, int bias_
 void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset,
                           int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
                           int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
-                          uint8_t* perm_exact, int4* mtiles, const SplitPolicy& sp, hipStream_t stream);
+                          uint8_t* perm_exact, int4* mtiles, int* counters, const SplitPolicy& sp,
+                          hipStream_t stream);
 
 // Pointers into the caller's workspace produced by routing + permutation.
 struct Plan {
@@ -53,6 +54,7 @@ struct Plan {
   const int4* mblocks2;       // large T, GEMM2: the same with class 0 and class 1 rows in separate
                               // blocks (one precision mode per block); info[5] blocks in all
   const int* canon_token;     // token of each pair in canonical (expert, token) order
+  int* counters;              // small T: arrivals per (m-tile, 128 C columns), zeroed by the permutation
 };
 
 struct Problem {
@@ -65,7 +67,8 @@ struct Problem {
   int T, E_local, H, I;
 };
 
-// Small-T path: GEMM1 partials -> activation (f16 hi/lo C) -> GEMM2 partials.
+// Small-T path: GEMM1 partials (+ SwiGLU into f16 hi/lo C by the last unit of each group)
+// -> GEMM2 partials.
 struct CHalf {
   _Float16* hi;   // [Pmax][I]
   _Float16* lo;   // [Pmax][I]
@@ -74,9 +77,7 @@ struct CHalf {
 int decode_grid1();
 int decode_grid2();
 int decode_unit_groups();
-void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, hipStream_t stream);
-void launch_activation_decode(const Problem& pb, const Plan& pl, const float* gbuf, const CHalf& ch, int pmax,
-                              hipStream_t stream);
+void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, const CHalf& ch, hipStream_t stream);
 void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, hipStream_t stream);
 
 // Large-T path (T > 64).  Permutation arguments: pair counts per (block of 256 tokens,

@@ -268,11 +268,14 @@ __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __rest
   }
 }
 
-// Largest K-split S in {8, 4, 2, 1} whose units still fit the grid and the partial rows.
+// K-split of a decode GEMM: the largest S in {8, 4, 2} whose units still fit the grid and
+// the partial rows, at least ceil(kb / 64) (a unit holds the weight scales of its <= 64
+// K-blocks one per lane), else that minimum.
 __device__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap) {
-  for (int S = 8; S > 1; S >>= 1)
+  const int s_min = (kb + kWave - 1) / kWave;
+  for (int S = 8; S > s_min; S >>= 1)
     if ((int64_t)n_mt * ncb * S <= slots && (int64_t)S * P <= rows_cap && S <= kb) return S;
-  return 1;
+  return s_min;
 }
 
 // Stable permutation for T <= 64 (one workgroup, one thread per (token, k) pair).  A 64-bit
@@ -292,7 +295,7 @@ __global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
     int* __restrict__ expert_offsets, int* __restrict__ perm_token, float* __restrict__ perm_w,
     int* __restrict__ tok_slot, int* __restrict__ active, int* __restrict__ mtile_offsets, int* __restrict__ info,
     const float* __restrict__ tok_a2, const float* __restrict__ esig, float sqrt_i, uint8_t* __restrict__ perm_exact,
-    int4* __restrict__ mtiles, SplitPolicy sp) {
+    int4* __restrict__ mtiles, int* __restrict__ counters, int groups, SplitPolicy sp) {
   __shared__ unsigned long long tmask[kEGlobal];
   __shared__ int base_s[kEGlobal];
   __shared__ int mtb_s[kEGlobal];                   // first m-tile of each local expert
@@ -376,15 +379,17 @@ __global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
   if (in && j >= n) tok_slot[t * kTopK + j] = -1;
   __syncthreads();
   for (int g = tid; g < n_mt_s; g += kSmallPermThreads) mtiles[g] = mt_s[g];
+  for (int i = tid; i < n_mt_s * groups; i += kSmallPermThreads) counters[i] = 0;
 }
 
 void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset,
                           int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
                           int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
-                          uint8_t* perm_exact, int4* mtiles, const SplitPolicy& sp, hipStream_t stream) {
+                          uint8_t* perm_exact, int4* mtiles, int* counters, const SplitPolicy& sp,
+                          hipStream_t stream) {
   hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(kSmallPermThreads), 0, stream, topk_ids, topk_w, T,
                      E_local, offset, expert_offsets, perm_token, perm_w, tok_slot, active, mtile_offsets, info,
-                     tok_a2, esig, sqrtf((float)I), perm_exact, mtiles, sp);
+                     tok_a2, esig, sqrtf((float)I), perm_exact, mtiles, counters, I / kBlock, sp);
 }
 
 void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
