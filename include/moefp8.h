@@ -93,7 +93,8 @@ typedef struct moefp8_args {
   /* optional, may be NULL: array of MOEFP8_NUM_STAGE_EVENTS hipEvent_t created by the
    * caller.  Event i is recorded on `stream` before stage i (route, permute, GEMM1,
    * activation, GEMM2, combine; GEMM1 applies SwiGLU itself, so the activation stage is
-   * empty) and the last one after the combine, so stage i's device time is
+   * empty, and for T <= 64 GEMM2 also does the combine, leaving that stage empty too) and
+   * the last one after the combine, so stage i's device time is
    * hipEventElapsedTime(ev[i], ev[i+1]).  Used for live per-kernel timing. */
   void* stage_events;
 } moefp8_args;

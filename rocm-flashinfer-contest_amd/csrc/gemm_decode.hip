@@ -21,8 +21,9 @@
 //             C = silu(sum_s G1[:, I:]) * sum_s G1[:, :I]              (main.py:232-233),
 //             stored as f16 hi + lo with one fp32 scale per (pair, 128 columns)
 // GEMM2       O partials = routing weight * C W2_e^T over a K-slice   (main.py:234-241),
-//             exact products of C's f16 hi term (2^-11 relative) and W2 widened to f16
-// The combine kernel then sums each token's pair rows and splits (main.py:242-243).
+//             exact products of C's f16 hi term (2^-11 relative) and W2 widened to f16;
+//             the last unit to finish a 64-column block then sums each token's pair rows
+//             and splits over those columns into the bf16 output   (main.py:241-243).
 // M-tiles flagged for exact products (GEMM1) or for both f16 terms of C (GEMM2) take a
 // simpler per-wavefront path.
 #include "moefp8_device.h"
@@ -256,15 +257,92 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
   }
 }
 
+// Combine of output columns [c0, c0 + 64) for every token by one workgroup (main.py:241-243):
+// each token's pair rows in ascending local-expert order (tok_slot), the K-split partials of
+// a row first, summed from zero in fp32 and rounded once to bf16; tokens without a local
+// expert get zeros.  Thread = (token, 4 columns).
+__device__ void combine_columns(const int* __restrict__ tok_slot, const float* __restrict__ obuf,
+                                uint16_t* __restrict__ out, int T, int H, int S, int c0) {
+  constexpr int kQuads = 16;                            // 4-column groups of the 64 columns
+  const int c = c0 + 4 * (threadIdx.x % kQuads);
+  for (int t = threadIdx.x / kQuads; t < T; t += blockDim.x / kQuads) {
+    int slots[kTopK];
+#pragma unroll
+    for (int k = 0; k < kTopK; k++) slots[k] = tok_slot[(size_t)t * kTopK + k];
+    float4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (S == 1) {
+      // the token's (at most 8) rows loaded together; a token's unused slots are -1 and last
+      float2 lo[kTopK], hi[kTopK];
+#pragma unroll
+      for (int k = 0; k < kTopK; k++) {
+        const float* r = obuf + (size_t)max(slots[k], 0) * H + c;
+        lo[k] = load_shared_f32x2(r);
+        hi[k] = load_shared_f32x2(r + 2);
+      }
+#pragma unroll
+      for (int k = 0; k < kTopK; k++) {
+        if (slots[k] >= 0) {
+          acc.x += lo[k].x;
+          acc.y += lo[k].y;
+          acc.z += hi[k].x;
+          acc.w += hi[k].y;
+        }
+      }
+    }
+    for (int k = 0; S > 1 && k < kTopK; k++) {
+      if (slots[k] < 0) break;
+      const float* row = obuf + (size_t)slots[k] * S * H + c;
+      float4 o = {0.f, 0.f, 0.f, 0.f};                 // the row's splits, in order
+      for (int s0 = 0; s0 < S; s0 += kTopK) {
+        float2 lo[kTopK], hi[kTopK];                    // up to 8 splits loaded together
+#pragma unroll
+        for (int q = 0; q < kTopK; q++) {
+          const float* r = row + (size_t)min(s0 + q, S - 1) * H;
+          lo[q] = load_shared_f32x2(r);
+          hi[q] = load_shared_f32x2(r + 2);
+        }
+#pragma unroll
+        for (int q = 0; q < kTopK; q++) {
+          if (s0 + q == 0) {
+            o = float4{lo[q].x, lo[q].y, hi[q].x, hi[q].y};
+          } else if (s0 + q < S) {
+            o.x += lo[q].x;
+            o.y += lo[q].y;
+            o.z += hi[q].x;
+            o.w += hi[q].y;
+          }
+        }
+      }
+      acc.x += o.x;
+      acc.y += o.y;
+      acc.z += o.z;
+      acc.w += o.w;
+    }
+    uint2 v;
+    v.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
+    v.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
+    *reinterpret_cast<uint2*>(out + (size_t)t * H + c) = v;
+  }
+}
+
 __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_decode_kernel(Problem pb, Plan pl,
                                                                                              CHalf ch,
-                                                                                             float* __restrict__ obuf) {
+                                                                                             float* __restrict__ obuf,
+                                                                                             uint16_t* __restrict__ out) {
   __shared__ G2Stage ring[2];
+  __shared__ int last_s;
   const int n_mt = pl.info[2], S = pl.info[4];
-  const int H = pb.H, I = pb.I;
+  const int H = pb.H, I = pb.I, T = pb.T;
   const int KB = I / kBlock, HB = H / kBlock, NCB = H / (16 * kDecBlockWaves);
   const int n_units = n_mt * S * NCB;
   const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  if (n_units == 0) {
+    // no local pairs: every output row is zero
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < (size_t)T * H / 4;
+         i += (size_t)gridDim.x * blockDim.x)
+      reinterpret_cast<uint2*>(out)[i] = uint2{0u, 0u};
+    return;
+  }
 
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
     const DecUnit du = decode_unit(u, S, NCB);
@@ -356,9 +434,13 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       const int row = 4 * kg + r;
       if (row < M) {
         const int p = row0 + row;
-        obuf[((size_t)p * S + du.s) * H + cg * 16 + lr] = acc[r] * pl.perm_w[p];
+        store_shared_f32(obuf + ((size_t)p * S + du.s) * H + cg * 16 + lr, acc[r] * pl.perm_w[p]);
       }
     }
+    // output columns [64 cb, 64 cb + 64) are complete once all n_mt * S units of the column
+    // block stored their rows
+    if (arrive_last(pl.counters2 + du.cb, n_mt * S, &last_s))
+      combine_columns(pl.tok_slot, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves);
   }
 }
 
@@ -373,9 +455,11 @@ void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, const C
                      ch);
 }
 
-void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, hipStream_t stream) {
+void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, uint16_t* out,
+                        hipStream_t stream) {
+  if (pb.T <= 0) return;
   hipLaunchKernelGGL(gemm2_decode_kernel, dim3(decode_grid2()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, ch,
-                     obuf);
+                     obuf, out);
 }
 
 }  // namespace moefp8

@@ -36,7 +36,7 @@ int large_rows_b(int64_t T, int H, int I) { return large_big(T, H, I) ? kExactRo
 
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
-  size_t tok_a2, esig, perm_exact, mtiles, counters, c16, c16_scale, gbuf, obuf;
+  size_t tok_a2, esig, perm_exact, mtiles, counters, counters2, c16, c16_scale, gbuf, obuf;
   size_t canon_token, bcnt, ccnt, mblocks1, mblocks2, c_hi, c_lo, c_lo16, c_scale;
   size_t total;
   int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks1, max_blocks2;
@@ -79,6 +79,7 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
     L.rows_cap = pmax * smin > r8 ? pmax * smin : r8;
     L.mtiles = take((size_t)L.max_mtiles * 16);
     L.counters = take((size_t)L.max_mtiles * (I / kBlock) * 4);
+    L.counters2 = take((size_t)(H / (16 * decode_unit_groups())) * 4);
     L.gbuf = take((size_t)L.rows_cap * 2 * I * 4);
     L.c16 = take((size_t)L.c_plane * 2 * 2);
     L.c16_scale = take((size_t)pmax * (I / kBlock) * 4);
@@ -260,6 +261,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pl.mblocks2 = nullptr;
   pl.canon_token = pl.perm_token;
   pl.counters = nullptr;
+  pl.counters2 = nullptr;
   float* tok_a2 = reinterpret_cast<float*>(ws + L.tok_a2);
   float* esig = reinterpret_cast<float*>(ws + L.esig);
 
@@ -282,12 +284,14 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   MagInputs mag = {a->hidden_states, a->hidden_states_scale, a->gemm1_weights_scale, a->gemm2_weights_scale,
                    H, I, E_local, tok_a2, esig};
   if (T <= kDecodeMaxT) {
-    // small T: routing (+ scale estimates), permutation, GEMM1 (+ SwiGLU), GEMM2, combine
+    // small T: routing (+ scale estimates), permutation, GEMM1 (+ SwiGLU), GEMM2 (+ combine)
     const int groups = decode_unit_groups();
     const SplitPolicy sp = {decode_grid1(), 2 * I / (16 * groups), H / kBlock, (int)L.rows_cap,
                             decode_grid2(), H / (16 * groups),     I / kBlock, (int)L.rows_cap};
     pl.mtiles = reinterpret_cast<const int4*>(ws + L.mtiles);
     pl.counters = reinterpret_cast<int*>(ws + L.counters);
+    pl.counters2 = reinterpret_cast<int*>(ws + L.counters2);
+    const int n_counters2 = H / (16 * groups);
     mark(0);
     launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,
                  topk_ids, topk_w, &mag, s);
@@ -296,7 +300,8 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
                          const_cast<int*>(pl.expert_offsets), const_cast<int*>(pl.perm_token),
                          const_cast<float*>(pl.perm_w), const_cast<int*>(pl.tok_slot), const_cast<int*>(pl.active),
                          const_cast<int*>(pl.mtile_offsets), const_cast<int*>(pl.info), tok_a2, esig, I,
-                         const_cast<uint8_t*>(pl.exact), const_cast<int4*>(pl.mtiles), pl.counters, sp, s);
+                         const_cast<uint8_t*>(pl.exact), const_cast<int4*>(pl.mtiles), pl.counters, pl.counters2,
+                         n_counters2, sp, s);
     mark(2);
     float* gbuf = reinterpret_cast<float*>(ws + L.gbuf);
     float* obuf = reinterpret_cast<float*>(ws + L.obuf);
@@ -307,10 +312,9 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
     launch_gemm1_decode(pb, pl, gbuf, ch, s);
     mark(3);
     mark(4);   // SwiGLU is GEMM1's epilogue: empty activation stage
-    launch_gemm2_decode(pb, pl, ch, obuf, s);
+    launch_gemm2_decode(pb, pl, ch, obuf, a->output, s);
     mark(5);
-    launch_combine(pl, obuf, a->output, (int)T, H, s);
-    mark(6);
+    mark(6);   // the combine is GEMM2's epilogue: empty combine stage
     return finish(a, L, topk_ids, topk_w, pl, s);
   }
   // large T: routing, permutation (3 launches), GEMM1 (+SwiGLU, C split), GEMM2, combine

@@ -34,8 +34,8 @@ void launch_route(const void* logits, int logits_dt, const void* bias, int bias_
 void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset,
                           int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
                           int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
-                          uint8_t* perm_exact, int4* mtiles, int* counters, const SplitPolicy& sp,
-                          hipStream_t stream);
+                          uint8_t* perm_exact, int4* mtiles, int* counters, int* counters2, int n_counters2,
+                          const SplitPolicy& sp, hipStream_t stream);
 
 // Pointers into the caller's workspace produced by routing + permutation.
 struct Plan {
@@ -55,6 +55,7 @@ struct Plan {
                               // blocks (one precision mode per block); info[5] blocks in all
   const int* canon_token;     // token of each pair in canonical (expert, token) order
   int* counters;              // small T: arrivals per (m-tile, 128 C columns), zeroed by the permutation
+  int* counters2;             // small T: arrivals per 64 output columns, zeroed by the permutation
 };
 
 struct Problem {
@@ -68,7 +69,7 @@ struct Problem {
 };
 
 // Small-T path: GEMM1 partials (+ SwiGLU into f16 hi/lo C by the last unit of each group)
-// -> GEMM2 partials.
+// -> GEMM2 partials (+ the combine into the bf16 output by the last unit of each column block).
 struct CHalf {
   _Float16* hi;   // [Pmax][I]
   _Float16* lo;   // [Pmax][I]
@@ -78,7 +79,8 @@ int decode_grid1();
 int decode_grid2();
 int decode_unit_groups();
 void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, const CHalf& ch, hipStream_t stream);
-void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, hipStream_t stream);
+void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, uint16_t* out,
+                        hipStream_t stream);
 
 // Large-T path (T > 64).  Permutation arguments: pair counts per (block of 256 tokens,
 // bucket = local expert x magnitude class) and the outputs of the three launches.

@@ -295,7 +295,8 @@ __global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
     int* __restrict__ expert_offsets, int* __restrict__ perm_token, float* __restrict__ perm_w,
     int* __restrict__ tok_slot, int* __restrict__ active, int* __restrict__ mtile_offsets, int* __restrict__ info,
     const float* __restrict__ tok_a2, const float* __restrict__ esig, float sqrt_i, uint8_t* __restrict__ perm_exact,
-    int4* __restrict__ mtiles, int* __restrict__ counters, int groups, SplitPolicy sp) {
+    int4* __restrict__ mtiles, int* __restrict__ counters, int groups, int* __restrict__ counters2, int n_counters2,
+    SplitPolicy sp) {
   __shared__ unsigned long long tmask[kEGlobal];
   __shared__ int base_s[kEGlobal];
   __shared__ int mtb_s[kEGlobal];                   // first m-tile of each local expert
@@ -380,16 +381,18 @@ __global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
   __syncthreads();
   for (int g = tid; g < n_mt_s; g += kSmallPermThreads) mtiles[g] = mt_s[g];
   for (int i = tid; i < n_mt_s * groups; i += kSmallPermThreads) counters[i] = 0;
+  for (int i = tid; i < n_counters2; i += kSmallPermThreads) counters2[i] = 0;
 }
 
 void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset,
                           int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
                           int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
-                          uint8_t* perm_exact, int4* mtiles, int* counters, const SplitPolicy& sp,
-                          hipStream_t stream) {
+                          uint8_t* perm_exact, int4* mtiles, int* counters, int* counters2, int n_counters2,
+                          const SplitPolicy& sp, hipStream_t stream) {
   hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(kSmallPermThreads), 0, stream, topk_ids, topk_w, T,
                      E_local, offset, expert_offsets, perm_token, perm_w, tok_slot, active, mtile_offsets, info,
-                     tok_a2, esig, sqrtf((float)I), perm_exact, mtiles, counters, I / kBlock, sp);
+                     tok_a2, esig, sqrtf((float)I), perm_exact, mtiles, counters, I / kBlock, counters2, n_counters2,
+                     sp);
 }
 
 void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
