@@ -1,0 +1,139 @@
+// Small-T (T <= 64) plan of the expert GEMMs, rebuilt in LDS by every workgroup of the
+// first GEMM from the routing outputs: the stable token -> local-expert permutation of
+// main.py:216-226 (for each local expert in ascending order, its tokens in ascending order,
+// as torch.nonzero gives them), the 16-row m-tile table and the K-splits of both GEMMs.
+// With at most 512 pairs this takes one round of L2 reads and a few LDS passes, less than
+// a separate launch; workgroup 0 also writes the global tables the second GEMM and the
+// caller's debug outputs read.
+#pragma once
+
+#include "moefp8_device.h"
+#include "moefp8_launch.h"
+
+namespace moefp8 {
+
+constexpr int kSmallT = 64;
+constexpr int kSmallTile = 16;
+constexpr int kSmallPairs = kSmallT * kTopK;
+constexpr int kSmallMaxMtiles = kSmallPairs / kSmallTile + kEGlobal;
+
+struct DecodePlanLds {
+  unsigned long long tmask[kEGlobal];   // tokens (bit t) that picked each local expert
+  int base[kEGlobal];                   // first pair row of each local expert
+  int mtb[kEGlobal];                    // first m-tile of each local expert
+  int4 mt[kSmallMaxMtiles];             // {expert, first pair row, rows, OR of pair flags}
+  int tok[kSmallPairs];                 // token of each pair row
+  int ids[kSmallPairs];                 // local expert of each (token, k) pair, -1 if none
+  int n_mt, P, S1, S2;
+};
+
+// K-split of a decode GEMM: the largest S in {8, 4, 2} whose units still fit the grid and
+// the partial rows, at least ceil(kb / 64) (a unit holds the weight scales of its <= 64
+// K-blocks one per lane), else that minimum.
+__device__ __forceinline__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap) {
+  const int s_min = (kb + kWave - 1) / kWave;
+  for (int S = 8; S > s_min; S >>= 1)
+    if ((int64_t)n_mt * ncb * S <= slots && (int64_t)S * P <= rows_cap && S <= kb) return S;
+  return s_min;
+}
+
+// Builds the plan in `L` (every thread of the workgroup takes part; ends with a barrier).
+// With `global`, also writes expert_offsets, active, mtile_offsets, info {P, active experts,
+// m-tiles, S1, S2}, perm_token, perm_w, tok_slot (each token's pair rows in ascending local
+// expert order, -1 past its last) and the m-tile table.
+__device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, bool global) {
+  const int tid = threadIdx.x, nth = blockDim.x, lane = lane_id(), wave = tid >> 6;
+  const int T = a.T, E = a.E_local, NP = T * kTopK;
+  for (int e = tid; e < E; e += nth) L.tmask[e] = 0ull;
+  __syncthreads();
+  for (int i = tid; i < NP; i += nth) {
+    const int le = a.topk_ids[i] - a.offset;
+    const bool local = le >= 0 && le < E;
+    L.ids[i] = local ? le : -1;
+    if (local) atomicOr(&L.tmask[le], 1ull << (i >> 3));
+  }
+  __syncthreads();
+
+  // per-expert counts -> pair offsets, m-tile offsets, active list (wave 0, ballot prefix sums)
+  if (wave == 0) {
+    int carry_p = 0, carry_mt = 0, carry_a = 0;
+    for (int e0 = 0; e0 < E; e0 += kWave) {
+      const int e = e0 + lane;
+      const int c = e < E ? __popcll(L.tmask[e]) : 0;
+      const int mt = (c + kSmallTile - 1) / kSmallTile;
+      int pc = 0, pm = 0;
+#pragma unroll
+      for (int bit = 0; bit < 7; bit++) {
+        pc += lanes_below(__ballot((c >> bit) & 1)) << bit;
+        pm += lanes_below(__ballot((mt >> bit) & 1)) << bit;
+      }
+      const uint64_t act = __ballot(c > 0);
+      if (e < E) {
+        L.base[e] = carry_p + pc;
+        L.mtb[e] = carry_mt + pm;
+        for (int j = 0; j < mt; j++)
+          L.mt[carry_mt + pm + j] = int4{e, carry_p + pc + kSmallTile * j, min(kSmallTile, c - kSmallTile * j), 0};
+        if (global) {
+          a.expert_offsets[e] = carry_p + pc;
+          a.mtile_offsets[e] = carry_mt + pm;
+          if (c > 0) a.active[carry_a + lanes_below(act)] = e;
+        }
+      }
+      carry_p += __builtin_amdgcn_readlane(pc + c, kWave - 1);
+      carry_mt += __builtin_amdgcn_readlane(pm + mt, kWave - 1);
+      carry_a += (int)__popcll(act);
+    }
+    if (lane == 0) {
+      L.P = carry_p;
+      L.n_mt = carry_mt;
+      L.S1 = pick_split(carry_mt, a.sp.ncb1, a.sp.kb1, a.sp.slots1, carry_p, a.sp.rows_cap1);
+      L.S2 = pick_split(carry_mt, a.sp.ncb2, a.sp.kb2, a.sp.slots2, carry_p, a.sp.rows_cap2);
+      if (global) {
+        a.expert_offsets[E] = carry_p;
+        a.mtile_offsets[E] = carry_mt;
+        a.info[0] = carry_p;
+        a.info[1] = carry_a;
+        a.info[2] = carry_mt;
+        a.info[3] = L.S1;
+        a.info[4] = L.S2;
+      }
+    }
+  }
+  __syncthreads();
+
+  // pair rows: rank of the token inside its expert (popcount of the lower tokens); the
+  // m-tile flags are the OR of its pairs' precision flags
+  for (int i0 = 0; i0 < NP; i0 += nth) {
+    const int i = i0 + tid;
+    const int t = i >> 3, j = i & 7;
+    const int le = i < NP ? L.ids[i] : -1;
+    // k = rank of this pair's local expert among its token's local experts (8 consecutive
+    // lanes hold one token): the combine adds a token's rows in ascending expert order
+    int k = 0, n_loc = 0;
+#pragma unroll
+    for (int q = 0; q < kTopK; q++) {
+      const int le_q = __shfl(le >= 0 ? le : kEGlobal, (lane & ~7) + q, kWave);
+      k += le_q < le ? 1 : 0;
+      n_loc += le_q < kEGlobal ? 1 : 0;
+    }
+    if (le >= 0) {
+      const int pos = L.base[le] + (int)__popcll(L.tmask[le] & ((1ull << t) - 1ull));
+      L.tok[pos] = t;
+      const float w = a.topk_w[i];
+      const float pred = predicted_output_rms(a.tok_a2[t], w, a.esig[2 * le], a.esig[2 * le + 1], a.sqrt_i);
+      const int flags = (pred > kPreciseRms ? kFlagExactProducts : 0) | (pred > kOneTermRms ? kFlagTwoTermC : 0);
+      if (flags) atomicOr(&L.mt[L.mtb[le] + (pos - L.base[le]) / kSmallTile].w, flags);
+      if (global) {
+        a.perm_token[pos] = t;
+        a.perm_w[pos] = w;
+        a.tok_slot[t * kTopK + k] = pos;
+      }
+    }
+    if (global && i < NP && j >= n_loc) a.tok_slot[t * kTopK + j] = -1;
+  }
+  __syncthreads();
+  if (global)
+    for (int g = tid; g < L.n_mt; g += nth) a.mtiles[g] = L.mt[g];
+}
+
+}  // namespace moefp8

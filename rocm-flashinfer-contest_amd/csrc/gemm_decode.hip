@@ -26,6 +26,7 @@
 //             and splits over those columns into the bf16 output   (main.py:241-243).
 // M-tiles flagged for exact products (GEMM1) or for both f16 terms of C (GEMM2) take a
 // simpler per-wavefront path.
+#include "decode_plan.h"
 #include "moefp8_device.h"
 #include "moefp8_launch.h"
 
@@ -144,11 +145,14 @@ __device__ __forceinline__ void swiglu_block(int I, int S, int p, int cb, const 
 }
 
 __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_decode_kernel(Problem pb, Plan pl,
+                                                                                             DecodePlanArgs da,
                                                                                              float* __restrict__ gbuf,
                                                                                              CHalf ch) {
   __shared__ G1Stage ring[2];
+  __shared__ DecodePlanLds plan;
   __shared__ int last_s;
-  const int n_mt = pl.info[2], S = pl.info[3];
+  build_decode_plan(da, plan, blockIdx.x == 0);
+  const int n_mt = plan.n_mt, S = plan.S1;
   const int H = pb.H, I = pb.I, I2 = 2 * pb.I, T = pb.T;
   const int KB = H / kBlock, NCB = I2 / (16 * kDecBlockWaves);
   const int n_units = n_mt * S * NCB;
@@ -156,7 +160,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
 
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
     const DecUnit du = decode_unit(u, S, NCB);
-    const int4 mt = pl.mtiles[du.g];
+    const int4 mt = plan.mt[du.g];
     const int e = uniform(mt.x), row0 = uniform(mt.y), M = uniform(mt.z), flags = uniform(mt.w);
     const int kb0 = du.s * KB / S, n = (du.s + 1) * KB / S - kb0;
     const int cg = du.cb * kDecBlockWaves + wave;
@@ -164,7 +168,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
     const uint8_t* bp = pb.w13 + ((size_t)e * I2 + cg * 16 + lr) * H + (size_t)kb0 * kBlock + kg * 32;
     const float* swp = pb.s13 + ((size_t)e * (I2 / kBlock) + (cg * 16) / kBlock) * KB + kb0;
     // rows >= M repeat the m-tile's first pair (real data, results discarded)
-    const int tok = pl.perm_token[row0 + (lr < M ? lr : 0)];
+    const int tok = plan.tok[row0 + (lr < M ? lr : 0)];
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 
     if (!(flags & kFlagExactProducts)) {
@@ -224,7 +228,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int dr = 4 * kg + r;
-        tok_d[r] = pl.perm_token[row0 + (dr < M ? dr : 0)];
+        tok_d[r] = plan.tok[row0 + (dr < M ? dr : 0)];
       }
       const uint8_t* ap = pb.hidden + (size_t)tok * H + (size_t)kb0 * kBlock + kg * 32;
       for (int j = 0; j < n; j++) {
@@ -450,9 +454,10 @@ int decode_grid1() { return num_compute_units() * kDec1BlocksPerCU; }
 int decode_grid2() { return num_compute_units() * kDec2BlocksPerCU; }
 int decode_unit_groups() { return kDecBlockWaves; }
 
-void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, const CHalf& ch, hipStream_t stream) {
-  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(decode_grid1()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, gbuf,
-                     ch);
+void launch_gemm1_decode(const Problem& pb, const Plan& pl, const DecodePlanArgs& da, float* gbuf, const CHalf& ch,
+                         hipStream_t stream) {
+  hipLaunchKernelGGL(gemm1_decode_kernel, dim3(decode_grid1()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, da,
+                     gbuf, ch);
 }
 
 void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, uint16_t* out,

@@ -36,10 +36,10 @@ int large_rows_b(int64_t T, int H, int I) { return large_big(T, H, I) ? kExactRo
 
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
-  size_t tok_a2, esig, perm_exact, mtiles, counters, counters2, c16, c16_scale, gbuf, obuf;
+  size_t tok_a2, esig, mtiles, counters, c16, c16_scale, gbuf, obuf;
   size_t canon_token, bcnt, ccnt, mblocks1, mblocks2, c_hi, c_lo, c_lo16, c_scale;
   size_t total;
-  int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks1, max_blocks2;
+  int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks1, max_blocks2, n_counters1, n_counters;
   int nblk;
 };
 
@@ -66,7 +66,6 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.tok_slot = take((size_t)T * kTopK * 4);
   L.tok_a2 = take((size_t)T * 4);
   L.esig = take((size_t)E_local * 2 * 4);
-  L.perm_exact = take((size_t)pmax);
   L.max_mtiles = (pmax + 15) / 16 + E_local;
   L.c_plane = (int64_t)align_up((size_t)pmax * I);
   if (T <= kDecodeMaxT) {
@@ -78,8 +77,10 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
     const int64_t kbmax = (H > I ? H : I) / kBlock, smin = (kbmax + 63) / 64;
     L.rows_cap = pmax * smin > r8 ? pmax * smin : r8;
     L.mtiles = take((size_t)L.max_mtiles * 16);
-    L.counters = take((size_t)L.max_mtiles * (I / kBlock) * 4);
-    L.counters2 = take((size_t)(H / (16 * decode_unit_groups())) * 4);
+    // arrival counters: per (m-tile, 128 C columns) for GEMM1, then per output column block
+    L.n_counters1 = L.max_mtiles * (I / kBlock);
+    L.n_counters = L.n_counters1 + H / (16 * decode_unit_groups());
+    L.counters = take((size_t)L.n_counters * 4);
     L.gbuf = take((size_t)L.rows_cap * 2 * I * 4);
     L.c16 = take((size_t)L.c_plane * 2 * 2);
     L.c16_scale = take((size_t)pmax * (I / kBlock) * 4);
@@ -215,7 +216,7 @@ int moefp8_route(const void* routing_logits, int32_t logits_dtype, const void* r
   if (query_device(&dev)) return MOEFP8_ERR_DEVICE;
   hipStream_t s = (hipStream_t)stream;
   launch_route(routing_logits, logits_dtype, routing_bias, bias_dtype, num_tokens, routed_scaling_factor, topk_ids,
-               topk_weights, nullptr, s);
+               topk_weights, nullptr, nullptr, 0, s);
   return hipGetLastError() == hipSuccess ? MOEFP8_OK : MOEFP8_ERR_LAUNCH;
 }
 
@@ -255,7 +256,6 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pl.active = reinterpret_cast<int*>(ws + L.active);
   pl.mtile_offsets = reinterpret_cast<int*>(ws + L.mtile_offsets);
   pl.info = reinterpret_cast<int*>(ws + L.info);
-  pl.exact = ws + L.perm_exact;
   pl.mtiles = nullptr;
   pl.mblocks1 = nullptr;
   pl.mblocks2 = nullptr;
@@ -284,32 +284,43 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   MagInputs mag = {a->hidden_states, a->hidden_states_scale, a->gemm1_weights_scale, a->gemm2_weights_scale,
                    H, I, E_local, tok_a2, esig};
   if (T <= kDecodeMaxT) {
-    // small T: routing (+ scale estimates), permutation, GEMM1 (+ SwiGLU), GEMM2 (+ combine)
+    // small T: routing (+ scale estimates), GEMM1 (+ permutation plan, SwiGLU), GEMM2 (+ combine)
     const int groups = decode_unit_groups();
     const SplitPolicy sp = {decode_grid1(), 2 * I / (16 * groups), H / kBlock, (int)L.rows_cap,
                             decode_grid2(), H / (16 * groups),     I / kBlock, (int)L.rows_cap};
     pl.mtiles = reinterpret_cast<const int4*>(ws + L.mtiles);
     pl.counters = reinterpret_cast<int*>(ws + L.counters);
-    pl.counters2 = reinterpret_cast<int*>(ws + L.counters2);
-    const int n_counters2 = H / (16 * groups);
+    pl.counters2 = pl.counters + L.n_counters1;
+    DecodePlanArgs da;
+    da.topk_ids = topk_ids;
+    da.topk_w = topk_w;
+    da.tok_a2 = tok_a2;
+    da.esig = esig;
+    da.T = (int)T;
+    da.E_local = E_local;
+    da.offset = a->local_expert_offset;
+    da.sqrt_i = sqrtf((float)I);
+    da.sp = sp;
+    da.expert_offsets = const_cast<int*>(pl.expert_offsets);
+    da.mtile_offsets = const_cast<int*>(pl.mtile_offsets);
+    da.active = const_cast<int*>(pl.active);
+    da.info = const_cast<int*>(pl.info);
+    da.perm_token = const_cast<int*>(pl.perm_token);
+    da.perm_w = const_cast<float*>(pl.perm_w);
+    da.tok_slot = const_cast<int*>(pl.tok_slot);
+    da.mtiles = const_cast<int4*>(pl.mtiles);
     mark(0);
     launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,
-                 topk_ids, topk_w, &mag, s);
+                 topk_ids, topk_w, &mag, pl.counters, (int)L.n_counters, s);
     mark(1);
-    launch_permute_small(topk_ids, topk_w, (int)T, E_local, a->local_expert_offset,
-                         const_cast<int*>(pl.expert_offsets), const_cast<int*>(pl.perm_token),
-                         const_cast<float*>(pl.perm_w), const_cast<int*>(pl.tok_slot), const_cast<int*>(pl.active),
-                         const_cast<int*>(pl.mtile_offsets), const_cast<int*>(pl.info), tok_a2, esig, I,
-                         const_cast<uint8_t*>(pl.exact), const_cast<int4*>(pl.mtiles), pl.counters, pl.counters2,
-                         n_counters2, sp, s);
-    mark(2);
+    mark(2);   // the permutation is rebuilt by every GEMM1 workgroup: empty permute stage
     float* gbuf = reinterpret_cast<float*>(ws + L.gbuf);
     float* obuf = reinterpret_cast<float*>(ws + L.obuf);
     CHalf ch;
     ch.hi = reinterpret_cast<_Float16*>(ws + L.c16);
     ch.lo = ch.hi + L.c_plane;
     ch.scale = reinterpret_cast<float*>(ws + L.c16_scale);
-    launch_gemm1_decode(pb, pl, gbuf, ch, s);
+    launch_gemm1_decode(pb, pl, da, gbuf, ch, s);
     mark(3);
     mark(4);   // SwiGLU is GEMM1's epilogue: empty activation stage
     launch_gemm2_decode(pb, pl, ch, obuf, a->output, s);
@@ -353,7 +364,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   float* obuf = reinterpret_cast<float*>(ws + L.obuf);
   mark(0);
   launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,
-               topk_ids, topk_w, &mag, s);
+               topk_ids, topk_w, &mag, nullptr, 0, s);
   mark(1);
   launch_permute_large(pa, s);
   mark(2);

@@ -25,17 +25,30 @@ struct SplitPolicy {
 };
 
 // Routing of every token (main.py:139-165): topk_ids [T,8] ascending, topk_w [T,8];
-// with `mag`, also the magnitude estimates.
+// with `mag`, also the magnitude estimates; zeroes zero[0, n_zero) (arrival counters of
+// the small-T GEMMs) on the way.
 void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
-                  int* topk_ids, float* topk_w, const MagInputs* mag, hipStream_t stream);
+                  int* topk_ids, float* topk_w, const MagInputs* mag, int* zero, int n_zero, hipStream_t stream);
 
-// The same permutation for T <= 64 in one workgroup with no serial loop, plus the
-// m-tile table (tile height 16) and the K-splits of the small-T GEMMs.
-void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset,
-                          int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
-                          int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
-                          uint8_t* perm_exact, int4* mtiles, int* counters, int* counters2, int n_counters2,
-                          const SplitPolicy& sp, hipStream_t stream);
+// Inputs and global outputs of the small-T plan (permutation of main.py:216-226, m-tiles
+// of height 16, K-splits) that the first small-T GEMM builds.
+struct DecodePlanArgs {
+  const int* topk_ids;
+  const float* topk_w;
+  const float* tok_a2;
+  const float* esig;
+  int T, E_local, offset;
+  float sqrt_i;
+  SplitPolicy sp;
+  int* expert_offsets;  // [E_local + 1]
+  int* mtile_offsets;   // [E_local + 1]
+  int* active;          // [E_local]
+  int* info;
+  int* perm_token;      // [Pmax]
+  float* perm_w;        // [Pmax]
+  int* tok_slot;        // [T * 8]
+  int4* mtiles;         // m-tile table
+};
 
 // Pointers into the caller's workspace produced by routing + permutation.
 struct Plan {
@@ -46,7 +59,6 @@ struct Plan {
   const int* active;          // [E_local]
   const int* mtile_offsets;   // [E_local + 1]
   const int* info;            // {P, n_active, GEMM1 m-blocks|m-tiles, S1, S2, GEMM2 m-blocks, m-tiles}
-  const uint8_t* exact;       // small T: [Pmax] per-pair flags (kFlagExactProducts, kFlagTwoTermC)
   const int4* mtiles;         // small T: per m-tile {expert, first pair, rows, OR of pair flags}
   const int4* mblocks1;       // large T, GEMM1: m-blocks {expert, first row, rows, flags}, expert by
                               // expert: its class 0 and 1 rows together, then its exact-product rows;
@@ -54,8 +66,8 @@ struct Plan {
   const int4* mblocks2;       // large T, GEMM2: the same with class 0 and class 1 rows in separate
                               // blocks (one precision mode per block); info[5] blocks in all
   const int* canon_token;     // token of each pair in canonical (expert, token) order
-  int* counters;              // small T: arrivals per (m-tile, 128 C columns), zeroed by the permutation
-  int* counters2;             // small T: arrivals per 64 output columns, zeroed by the permutation
+  int* counters;              // small T: arrivals per (m-tile, 128 C columns), zeroed by the routing
+  int* counters2;             // small T: arrivals per 64 output columns, zeroed by the routing
 };
 
 struct Problem {
@@ -78,7 +90,8 @@ struct CHalf {
 int decode_grid1();
 int decode_grid2();
 int decode_unit_groups();
-void launch_gemm1_decode(const Problem& pb, const Plan& pl, float* gbuf, const CHalf& ch, hipStream_t stream);
+void launch_gemm1_decode(const Problem& pb, const Plan& pl, const DecodePlanArgs& da, float* gbuf, const CHalf& ch,
+                         hipStream_t stream);
 void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, uint16_t* out,
                         hipStream_t stream);
 

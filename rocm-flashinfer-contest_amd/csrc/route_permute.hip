@@ -1,14 +1,11 @@
-// DeepSeek-V3 no-aux grouped routing and the deterministic token -> local-expert
-// permutation, for gfx950 wave64.
+// DeepSeek-V3 no-aux grouped routing for gfx950 wave64.
 //
 // route_kernel   restates solutions/moe_fp8/main.py:139-165 (_route) in the
 //                canonical arithmetic of the oracle: fp64-evaluated sigmoid rounded
 //                once to fp32, (value desc, index asc) ranking for groups and
 //                experts, ascending-id output, sequential fp32 normaliser.
-// permute_small_kernel restates the selection of main.py:216-226 for T <= 64: for
-//                each local expert in ascending order, the tokens that picked it in
-//                ascending token order (torch.nonzero), as one stable counting sort
-//                (larger T: permute_large.hip).
+// The token -> local-expert permutation that follows (main.py:216-226) is rebuilt by the
+// first small-T GEMM itself (decode_plan.h) or by permute_large.hip.
 #include "moefp8_device.h"
 #include "moefp8_launch.h"
 
@@ -238,11 +235,12 @@ __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __rest
                                                               const void* __restrict__ bias, int bias_dt, int64_t T,
                                                               float rsf, int* __restrict__ topk_ids,
                                                               float* __restrict__ topk_w, int token_blocks,
-                                                              MagArgs mg) {
+                                                              MagArgs mg, int* __restrict__ zero, int n_zero) {
   if ((int)blockIdx.x >= token_blocks) {
     expert_sigma_block(mg, blockIdx.x - token_blocks);
     return;
   }
+  for (int i = blockIdx.x * kSigmaThreads + threadIdx.x; i < n_zero; i += token_blocks * kSigmaThreads) zero[i] = 0;
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
   constexpr int kWavesPerBlock = kSigmaThreads / kWave;
@@ -268,135 +266,8 @@ __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __rest
   }
 }
 
-// K-split of a decode GEMM: the largest S in {8, 4, 2} whose units still fit the grid and
-// the partial rows, at least ceil(kb / 64) (a unit holds the weight scales of its <= 64
-// K-blocks one per lane), else that minimum.
-__device__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap) {
-  const int s_min = (kb + kWave - 1) / kWave;
-  for (int S = 8; S > s_min; S >>= 1)
-    if ((int64_t)n_mt * ncb * S <= slots && (int64_t)S * P <= rows_cap && S <= kb) return S;
-  return s_min;
-}
-
-// Stable permutation for T <= 64 (one workgroup, one thread per (token, k) pair).  A 64-bit
-// LDS mask of the tokens that picked each local expert gives its count (popcount) and each
-// pair's rank inside the expert (popcount of the lower tokens), so pairs come out
-// expert-major and token-ascending as in main.py:218-225 with no serial loop; the offsets
-// are exclusive prefix sums built from one ballot per bit (counts are <= 64).  Also
-// writes the m-tile table {expert, first pair, rows} (tile height 16) and the GEMM
-// K-splits.
-constexpr int kSmallT = 64;
-constexpr int kSmallTile = 16;
-constexpr int kSmallPermThreads = kSmallT * kTopK;
-constexpr int kSmallMaxMtiles = kSmallPermThreads / kSmallTile + kEGlobal;
-
-__global__ __launch_bounds__(kSmallPermThreads) void permute_small_kernel(
-    const int* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int E_local, int offset,
-    int* __restrict__ expert_offsets, int* __restrict__ perm_token, float* __restrict__ perm_w,
-    int* __restrict__ tok_slot, int* __restrict__ active, int* __restrict__ mtile_offsets, int* __restrict__ info,
-    const float* __restrict__ tok_a2, const float* __restrict__ esig, float sqrt_i, uint8_t* __restrict__ perm_exact,
-    int4* __restrict__ mtiles, int* __restrict__ counters, int groups, int* __restrict__ counters2, int n_counters2,
-    SplitPolicy sp) {
-  __shared__ unsigned long long tmask[kEGlobal];
-  __shared__ int base_s[kEGlobal];
-  __shared__ int mtb_s[kEGlobal];                   // first m-tile of each local expert
-  __shared__ int4 mt_s[kSmallMaxMtiles];            // {expert, first pair, rows, OR of pair flags}
-  __shared__ int n_mt_s;
-  const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-  const int t = tid >> 3, j = tid & 7;
-  const bool in = t < T;
-  int le = -1;
-  float w = 0.f, a2 = 0.f;
-  if (in) {
-    le = topk_ids[tid] - offset;
-    w = topk_w[tid];
-    a2 = tok_a2[t];
-  }
-  const bool local = in && le >= 0 && le < E_local;
-  for (int e = tid; e < E_local; e += kSmallPermThreads) tmask[e] = 0ull;
-  __syncthreads();
-  if (local) atomicOr(&tmask[le], 1ull << t);
-  __syncthreads();
-
-  if (wave == 0) {
-    int carry_p = 0, carry_mt = 0, carry_a = 0;
-    for (int e0 = 0; e0 < E_local; e0 += kWave) {
-      const int e = e0 + lane;
-      const int c = e < E_local ? __popcll(tmask[e]) : 0;
-      const int mt = (c + kSmallTile - 1) / kSmallTile;
-      int pc = 0, pm = 0;
-#pragma unroll
-      for (int bit = 0; bit < 7; bit++) {
-        pc += lanes_below(__ballot((c >> bit) & 1)) << bit;
-        pm += lanes_below(__ballot((mt >> bit) & 1)) << bit;
-      }
-      const uint64_t act = __ballot(c > 0);
-      if (e < E_local) {
-        expert_offsets[e] = carry_p + pc;
-        mtile_offsets[e] = carry_mt + pm;
-        base_s[e] = carry_p + pc;
-        if (c > 0) active[carry_a + lanes_below(act)] = e;
-        mtb_s[e] = carry_mt + pm;
-        for (int j = 0; j < mt; j++)
-          mt_s[carry_mt + pm + j] = int4{e, carry_p + pc + kSmallTile * j, min(kSmallTile, c - kSmallTile * j), 0};
-      }
-      carry_p += __builtin_amdgcn_readlane(pc + c, kWave - 1);
-      carry_mt += __builtin_amdgcn_readlane(pm + mt, kWave - 1);
-      carry_a += (int)__popcll(act);
-    }
-    if (lane == 0) {
-      expert_offsets[E_local] = carry_p;
-      mtile_offsets[E_local] = carry_mt;
-      info[0] = carry_p;    // P
-      info[1] = carry_a;    // active experts
-      info[2] = carry_mt;   // m-tiles of height 16
-      info[3] = pick_split(carry_mt, sp.ncb1, sp.kb1, sp.slots1, carry_p, sp.rows_cap1);
-      info[4] = pick_split(carry_mt, sp.ncb2, sp.kb2, sp.slots2, carry_p, sp.rows_cap2);
-      n_mt_s = carry_mt;
-    }
-  }
-  __syncthreads();
-
-  // k = rank of this pair's local expert among its token's local experts (a wave holds 8 whole
-  // tokens, lanes 8t'..8t'+7): the combine adds a token's rows in ascending expert order
-  const uint32_t tb = (uint32_t)(__ballot(local) >> (8 * (lane >> 3))) & 0xffu;
-  const int n = __popc(tb);
-  int k = 0;
-#pragma unroll
-  for (int q = 0; q < kTopK; q++) {
-    const int le_q = __shfl(local ? le : kEGlobal, (lane & ~7) + q, kWave);
-    k += le_q < le ? 1 : 0;
-  }
-  if (local) {
-    const int pos = base_s[le] + (int)__popcll(tmask[le] & ((1ull << t) - 1ull));
-    perm_token[pos] = t;
-    perm_w[pos] = w;
-    const float pred = predicted_output_rms(a2, w, esig[2 * le], esig[2 * le + 1], sqrt_i);
-    const int flags = (pred > kPreciseRms ? kFlagExactProducts : 0) | (pred > kOneTermRms ? kFlagTwoTermC : 0);
-    perm_exact[pos] = (uint8_t)flags;
-    tok_slot[t * kTopK + k] = pos;
-    if (flags) atomicOr(&mt_s[mtb_s[le] + (pos - base_s[le]) / kSmallTile].w, flags);
-  }
-  if (in && j >= n) tok_slot[t * kTopK + j] = -1;
-  __syncthreads();
-  for (int g = tid; g < n_mt_s; g += kSmallPermThreads) mtiles[g] = mt_s[g];
-  for (int i = tid; i < n_mt_s * groups; i += kSmallPermThreads) counters[i] = 0;
-  for (int i = tid; i < n_counters2; i += kSmallPermThreads) counters2[i] = 0;
-}
-
-void launch_permute_small(const int* topk_ids, const float* topk_w, int T, int E_local, int offset,
-                          int* expert_offsets, int* perm_token, float* perm_w, int* tok_slot, int* active,
-                          int* mtile_offsets, int* info, const float* tok_a2, const float* esig, int I,
-                          uint8_t* perm_exact, int4* mtiles, int* counters, int* counters2, int n_counters2,
-                          const SplitPolicy& sp, hipStream_t stream) {
-  hipLaunchKernelGGL(permute_small_kernel, dim3(1), dim3(kSmallPermThreads), 0, stream, topk_ids, topk_w, T,
-                     E_local, offset, expert_offsets, perm_token, perm_w, tok_slot, active, mtile_offsets, info,
-                     tok_a2, esig, sqrtf((float)I), perm_exact, mtiles, counters, I / kBlock, counters2, n_counters2,
-                     sp);
-}
-
 void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
-                  int* topk_ids, float* topk_w, const MagInputs* mag, hipStream_t stream) {
+                  int* topk_ids, float* topk_w, const MagInputs* mag, int* zero, int n_zero, hipStream_t stream) {
   if (T <= 0) return;
   const int64_t tokens_per_block = kSigmaThreads / kWave;
   int64_t blocks = (T + tokens_per_block - 1) / tokens_per_block;
@@ -416,7 +287,7 @@ void launch_route(const void* logits, int logits_dt, const void* bias, int bias_
     extra = mag->E_local;
   }
   hipLaunchKernelGGL(route_kernel, dim3((unsigned)(blocks + extra)), dim3(kSigmaThreads), 0, stream, logits, logits_dt,
-                     bias, bias_dt, T, rsf, topk_ids, topk_w, (int)blocks, mg);
+                     bias, bias_dt, T, rsf, topk_ids, topk_w, (int)blocks, mg, zero, n_zero);
 }
 
 
