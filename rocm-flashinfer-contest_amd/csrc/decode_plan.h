@@ -17,14 +17,18 @@ constexpr int kSmallTile = 16;
 constexpr int kSmallPairs = kSmallT * kTopK;
 constexpr int kSmallMaxMtiles = kSmallPairs / kSmallTile + kEGlobal;
 
+// What the GEMM reads while it runs ...
 struct DecodePlanLds {
+  int4 mt[kSmallMaxMtiles];             // {expert, first pair row, rows, OR of pair flags}
+  int tok[kSmallPairs];                 // token of each pair row
+  int n_mt, P, S1, S2;
+};
+// ... and what only the build uses (free for other use once it returns).
+struct DecodePlanScratch {
   unsigned long long tmask[kEGlobal];   // tokens (bit t) that picked each local expert
   int base[kEGlobal];                   // first pair row of each local expert
   int mtb[kEGlobal];                    // first m-tile of each local expert
-  int4 mt[kSmallMaxMtiles];             // {expert, first pair row, rows, OR of pair flags}
-  int tok[kSmallPairs];                 // token of each pair row
   int ids[kSmallPairs];                 // local expert of each (token, k) pair, -1 if none
-  int n_mt, P, S1, S2;
 };
 
 // K-split of a decode GEMM: the largest S in {8, 4, 2} whose units still fit the grid and
@@ -37,20 +41,21 @@ __device__ __forceinline__ int pick_split(int n_mt, int ncb, int kb, int slots, 
   return s_min;
 }
 
-// Builds the plan in `L` (every thread of the workgroup takes part; ends with a barrier).
+// Builds the plan in `L` using `X` (every thread of the workgroup takes part; ends with a
+// barrier).
 // With `global`, also writes expert_offsets, active, mtile_offsets, info {P, active experts,
 // m-tiles, S1, S2}, perm_token, perm_w, tok_slot (each token's pair rows in ascending local
 // expert order, -1 past its last) and the m-tile table.
-__device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, bool global) {
+__device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, DecodePlanScratch& X, bool global) {
   const int tid = threadIdx.x, nth = blockDim.x, lane = lane_id(), wave = tid >> 6;
   const int T = a.T, E = a.E_local, NP = T * kTopK;
-  for (int e = tid; e < E; e += nth) L.tmask[e] = 0ull;
+  for (int e = tid; e < E; e += nth) X.tmask[e] = 0ull;
   __syncthreads();
   for (int i = tid; i < NP; i += nth) {
     const int le = a.topk_ids[i] - a.offset;
     const bool local = le >= 0 && le < E;
-    L.ids[i] = local ? le : -1;
-    if (local) atomicOr(&L.tmask[le], 1ull << (i >> 3));
+    X.ids[i] = local ? le : -1;
+    if (local) atomicOr(&X.tmask[le], 1ull << (i >> 3));
   }
   __syncthreads();
 
@@ -59,7 +64,7 @@ __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, boo
     int carry_p = 0, carry_mt = 0, carry_a = 0;
     for (int e0 = 0; e0 < E; e0 += kWave) {
       const int e = e0 + lane;
-      const int c = e < E ? __popcll(L.tmask[e]) : 0;
+      const int c = e < E ? __popcll(X.tmask[e]) : 0;
       const int mt = (c + kSmallTile - 1) / kSmallTile;
       int pc = 0, pm = 0;
 #pragma unroll
@@ -69,8 +74,8 @@ __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, boo
       }
       const uint64_t act = __ballot(c > 0);
       if (e < E) {
-        L.base[e] = carry_p + pc;
-        L.mtb[e] = carry_mt + pm;
+        X.base[e] = carry_p + pc;
+        X.mtb[e] = carry_mt + pm;
         for (int j = 0; j < mt; j++)
           L.mt[carry_mt + pm + j] = int4{e, carry_p + pc + kSmallTile * j, min(kSmallTile, c - kSmallTile * j), 0};
         if (global) {
@@ -106,7 +111,7 @@ __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, boo
   for (int i0 = 0; i0 < NP; i0 += nth) {
     const int i = i0 + tid;
     const int t = i >> 3, j = i & 7;
-    const int le = i < NP ? L.ids[i] : -1;
+    const int le = i < NP ? X.ids[i] : -1;
     // k = rank of this pair's local expert among its token's local experts (8 consecutive
     // lanes hold one token): the combine adds a token's rows in ascending expert order
     int k = 0, n_loc = 0;
@@ -117,12 +122,12 @@ __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, boo
       n_loc += le_q < kEGlobal ? 1 : 0;
     }
     if (le >= 0) {
-      const int pos = L.base[le] + (int)__popcll(L.tmask[le] & ((1ull << t) - 1ull));
+      const int pos = X.base[le] + (int)__popcll(X.tmask[le] & ((1ull << t) - 1ull));
       L.tok[pos] = t;
       const float w = a.topk_w[i];
       const float pred = predicted_output_rms(a.tok_a2[t], w, a.esig[2 * le], a.esig[2 * le + 1], a.sqrt_i);
       const int flags = (pred > kPreciseRms ? kFlagExactProducts : 0) | (pred > kOneTermRms ? kFlagTwoTermC : 0);
-      if (flags) atomicOr(&L.mt[L.mtb[le] + (pos - L.base[le]) / kSmallTile].w, flags);
+      if (flags) atomicOr(&L.mt[X.mtb[le] + (pos - X.base[le]) / kSmallTile].w, flags);
       if (global) {
         a.perm_token[pos] = t;
         a.perm_w[pos] = w;

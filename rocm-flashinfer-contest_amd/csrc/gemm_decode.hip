@@ -68,6 +68,18 @@ struct alignas(16) G1Stage {
   float sa[16];
 };
 
+// Activation rows of an m-tile with at most kPreRows rows, staged once per unit for its
+// whole K-range (<= kPreMaxKB K-blocks) with their scales: the weight stream then runs
+// without a barrier per K step.  In decode most m-tiles hold one or two pairs.  Rows are
+// 64 bytes longer than their data, so equal offsets of different rows fall 16 banks apart.
+constexpr int kPreRows = 4;
+constexpr int kPreMaxKB = 32;
+constexpr int kPre1RowBytes = kPreMaxKB * kBlock + 64;
+struct alignas(16) G1Pre {
+  uint8_t a[kPreRows * kPre1RowBytes];
+  float sa[kPreMaxKB][kPreRows];
+};
+
 // LDS stage of GEMM2: 16 rows of C's f16 hi term x 128 columns, same chunk-major order.
 struct alignas(16) G2Stage {
   _Float16 a[16 * 16 * 8];
@@ -148,17 +160,28 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
                                                                                              DecodePlanArgs da,
                                                                                              float* __restrict__ gbuf,
                                                                                              CHalf ch) {
-  __shared__ G1Stage ring[2];
+  // the plan's build scratch, the per-step ring and the staged rows are never live together
+  __shared__ union {
+    DecodePlanScratch plan_x;
+    G1Stage ring[2];
+    G1Pre pre;
+  } sh;
   __shared__ DecodePlanLds plan;
   __shared__ int last_s;
-  build_decode_plan(da, plan, blockIdx.x == 0);
+  G1Stage* ring = sh.ring;
+  build_decode_plan(da, plan, sh.plan_x, blockIdx.x == 0);
   const int n_mt = plan.n_mt, S = plan.S1;
   const int H = pb.H, I = pb.I, I2 = 2 * pb.I, T = pb.T;
   const int KB = H / kBlock, NCB = I2 / (16 * kDecBlockWaves);
   const int n_units = n_mt * S * NCB;
-  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  const int wave = wave_index();
 
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
+    // lane-dependent addresses are formed per unit: hoisted in front of the loop they stay
+    // live across all three paths and spill
+    int lane = lane_id();
+    asm volatile("" : "+v"(lane));
+    const int lr = lane & 15, kg = lane >> 4;
     const DecUnit du = decode_unit(u, S, NCB);
     const int4 mt = plan.mt[du.g];
     const int e = uniform(mt.x), row0 = uniform(mt.y), M = uniform(mt.z), flags = uniform(mt.w);
@@ -171,27 +194,92 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
     const int tok = plan.tok[row0 + (lr < M ? lr : 0)];
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 
-    if (!(flags & kFlagExactProducts)) {
-      // carriers: waves 0/1 publish 16-byte chunk 4q + kg of row lr, wave 0's lanes < 16 the
-      // scale of row lane.  Every wavefront issues the same loads kDecDepth steps ahead
-      // (waves 2/3 repeat waves 0/1's, cache hits): loads under a branch would make the
-      // compiler's wait counting fall back to draining all of them.
-      const uint8_t* asrc = pb.hidden + (size_t)tok * H + (size_t)kb0 * kBlock + (4 * (wave & 1) + kg) * 16;
+    if (!(flags & kFlagExactProducts) && M <= kPreRows && n <= kPreMaxKB) {
+      const float swv = swp[min(lane, n - 1)];
+      v8i B[kDecDepth];
+      auto load = [&](int d, int j) { B[d] = load_v8i(bp + (size_t)min(j, n - 1) * kBlock); };
+#pragma unroll
+      for (int d = 0; d < kDecDepth; d++) load(d, d);
+      {
+        // rows [0, M) x K-blocks [kb0, kb0 + n) in 16-byte chunks (<= 4 per thread), then the
+        // M x n scales (<= 128), all loads issued before the first store
+        constexpr int kPer = kPreRows * kPreMaxKB * (kBlock / 16) / (64 * kDecBlockWaves);
+        const int nch = M * n * (kBlock / 16);
+        v4i v[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+          const int i = min((int)threadIdx.x + q * 64 * kDecBlockWaves, nch - 1);
+          const int r = i / (n * 8), c = i - r * n * 8;
+          v[q] = *reinterpret_cast<const v4i*>(pb.hidden + (size_t)plan.tok[row0 + r] * H + (size_t)kb0 * kBlock +
+                                               c * 16);
+        }
+        const int si = min((int)threadIdx.x, M * n - 1), sr = si / n, sj = si - sr * n;
+        const float sv = pb.hscale[(size_t)(kb0 + sj) * T + plan.tok[row0 + sr]];
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+          const int i = threadIdx.x + q * 64 * kDecBlockWaves;
+          const int r = i / (n * 8), c = i - r * n * 8;
+          if (i < nch) *reinterpret_cast<v4i*>(sh.pre.a + r * kPre1RowBytes + c * 16) = v[q];
+        }
+        if ((int)threadIdx.x < M * n) sh.pre.sa[sj][sr] = sv;
+        __syncthreads();
+      }
+      // rows >= M read row M - 1 (real data, results discarded)
+      const uint8_t* arow = sh.pre.a + min(lr, M - 1) * kPre1RowBytes + kg * 32;
+      auto step = [&](int d, int j) {
+        const v4i x = *reinterpret_cast<const v4i*>(arow + j * kBlock);
+        const v4i y = *reinterpret_cast<const v4i*>(arow + j * kBlock + 16);
+        const float4 sa = *reinterpret_cast<const float4*>(sh.pre.sa[j]);   // rows 0..3 (lanes kg = 0)
+        const float sw = readlane_f32(swv, j);
+        const v4f p = mfma16x16x128(__builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7), B[d],
+                                    v4f{0.f, 0.f, 0.f, 0.f});
+        acc[0] += p[0] * (sa.x * sw);
+        acc[1] += p[1] * (sa.y * sw);
+        acc[2] += p[2] * (sa.z * sw);
+        acc[3] += p[3] * (sa.w * sw);
+      };
+      int j = 0;
+      for (; j + kDecDepth <= n; j += kDecDepth) {
+#pragma unroll
+        for (int d = 0; d < kDecDepth; d++) {
+          step(d, j + d);
+          load(d, j + d + kDecDepth);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < kDecDepth - 1; d++)
+        if (j + d < n) step(d, j + d);
+      // the next unit restages only after every wavefront has read this one's rows
+      __syncthreads();
+    } else if (!(flags & kFlagExactProducts)) {
+      constexpr int kStepDepth = 2;   // (register budget shared with the staged path)
+      // carriers: waves 0/1 load rows 8q .. 8q + 7 of the activation block as whole 128-byte
+      // lines (lane l: row 8q + l/8, 16-byte chunk l%8) and publish them chunk-major; wave 0's
+      // lanes < 16 publish the scale of row lane.  Waves 2/3 issue as many loads, from one
+      // fixed line (loads under a branch would make the compiler's wait counting fall back to
+      // draining all of them).  Activation loads in the MFMA layout by every wavefront (16
+      // rows x 64 bytes per instruction) cost the weight stream ~20% (measured).
+      const int ar = 8 * (wave & 1) + (lane >> 3);
+      const int atok = plan.tok[row0 + (ar < M ? ar : 0)];
+      const uint8_t* asrc =
+          wave < 2 ? pb.hidden + (size_t)atok * H + (size_t)kb0 * kBlock + (lane & 7) * 16 : pb.hidden;
+      const int astep = wave < 2 ? kBlock : 0;
       const float* ssrc = pb.hscale + (size_t)kb0 * T + tok;
       // weight scale of K-block kb0 + l in lane l (n <= 64), read per step with readlane
       const float swv = swp[min(lane, n - 1)];
-      v8i B[kDecDepth];
-      v4i AR[kDecDepth];
-      float SR[kDecDepth];
+      v8i B[kStepDepth];
+      v4i AR[kStepDepth];
+      float SR[kStepDepth];
       auto load = [&](int d, int j) {
         const int jj = min(j, n - 1);
         B[d] = load_v8i(bp + (size_t)jj * kBlock);
-        AR[d] = *reinterpret_cast<const v4i*>(asrc + (size_t)jj * kBlock);
+        AR[d] = *reinterpret_cast<const v4i*>(asrc + (size_t)jj * astep);
         SR[d] = ssrc[(size_t)jj * T];
       };
       auto step = [&](int d, int j) {
         G1Stage& st = ring[j & 1];
-        if (wave < 2) *reinterpret_cast<v4i*>(st.a + wave * 1024 + lane * 16) = AR[d];
+        if (wave < 2) *reinterpret_cast<v4i*>(st.a + ((lane & 7) * 16 + ar) * 16) = AR[d];
         if (wave == 0 && lane < 16) st.sa[lane] = SR[d];
         __syncthreads();
         const v4i x = *reinterpret_cast<const v4i*>(st.a + ((2 * kg) * 16 + lr) * 16);
@@ -206,20 +294,20 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
         acc[3] += p[3] * (sa.w * sw);
       };
 #pragma unroll
-      for (int d = 0; d < kDecDepth; d++) load(d, d);
-      // full groups of kDecDepth steps (no early exit, so every prefetch stays where it is
-      // written), then the remaining < kDecDepth steps from the ring without new loads
+      for (int d = 0; d < kStepDepth; d++) load(d, d);
+      // full groups of kStepDepth steps (no early exit, so every prefetch stays where it is
+      // written), then the remaining < kStepDepth steps from the ring without new loads
       int j = 0;
-      for (; j + kDecDepth <= n; j += kDecDepth) {
+      for (; j + kStepDepth <= n; j += kStepDepth) {
 #pragma unroll
-        for (int d = 0; d < kDecDepth; d++) {
+        for (int d = 0; d < kStepDepth; d++) {
           step(d, j + d);
-          load(d, j + d + kDecDepth);
+          load(d, j + d + kStepDepth);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
 #pragma unroll
-      for (int d = 0; d < kDecDepth - 1; d++)
+      for (int d = 0; d < kStepDepth - 1; d++)
         if (j + d < n) step(d, j + d);
       // the next unit writes stage 0 only after every wavefront has read this unit's last stage
       __syncthreads();
@@ -360,9 +448,11 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 
     if (!(flags & kFlagTwoTermC)) {
-      // carriers: wave q publishes 16-byte chunk 4q + kg of row lr of C's hi term, wave 0's
-      // lanes < 16 the scale of row lane (all lanes load it: no loads under a branch)
-      const _Float16* asrc = ch.hi + (size_t)prow * I + (size_t)kb0 * kBlock + (4 * wave + kg) * 8;
+      // carriers: wave q loads rows 4q .. 4q + 3 of C's hi term as whole lines (lane l: row
+      // 4q + l/16, 16-byte chunk l%16) and publishes them chunk-major; wave 0's lanes < 16 the
+      // scale of row lane (all lanes load it: no loads under a branch)
+      const int ar = 4 * wave + (lane >> 4);
+      const _Float16* asrc = ch.hi + (size_t)(row0 + (ar < M ? ar : 0)) * I + (size_t)kb0 * kBlock + (lane & 15) * 8;
       const float* ssrc = ch.scale + (size_t)prow * KB + kb0;
       const float swv = swp[min(lane, n - 1)];
       v8i B[kDecDepth];
@@ -376,7 +466,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       };
       auto step = [&](int d, int j) {
         G2Stage& st = ring[j & 1];
-        *reinterpret_cast<v4i*>(st.a + wave * 512 + lane * 8) = AR[d];
+        *reinterpret_cast<v4i*>(st.a + ((lane & 15) * 16 + ar) * 8) = AR[d];
         if (wave == 0 && lane < 16) st.sa[lane] = SR[d];
         __syncthreads();
         v8h ah[4];
