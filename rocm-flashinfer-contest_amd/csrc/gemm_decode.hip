@@ -80,6 +80,14 @@ struct alignas(16) G1Pre {
   float sa[kPreMaxKB][kPreRows];
 };
 
+// GEMM2's staged rows: C's f16 hi term, <= kPre2MaxKB K-blocks of 128 columns per unit.
+constexpr int kPre2MaxKB = 16;
+constexpr int kPre2RowBytes = kPre2MaxKB * kBlock * 2 + 64;
+struct alignas(16) G2Pre {
+  uint8_t a[kPreRows * kPre2RowBytes];
+  float sa[kPre2MaxKB][kPreRows];
+};
+
 // LDS stage of GEMM2: 16 rows of C's f16 hi term x 128 columns, same chunk-major order.
 struct alignas(16) G2Stage {
   _Float16 a[16 * 16 * 8];
@@ -421,13 +429,17 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
                                                                                              CHalf ch,
                                                                                              float* __restrict__ obuf,
                                                                                              uint16_t* __restrict__ out) {
-  __shared__ G2Stage ring[2];
+  __shared__ union {
+    G2Stage ring[2];
+    G2Pre pre;
+  } sh;
   __shared__ int last_s;
+  G2Stage* ring = sh.ring;
   const int n_mt = pl.info[2], S = pl.info[4];
   const int H = pb.H, I = pb.I, T = pb.T;
   const int KB = I / kBlock, HB = H / kBlock, NCB = H / (16 * kDecBlockWaves);
   const int n_units = n_mt * S * NCB;
-  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  const int wave = wave_index();
   if (n_units == 0) {
     // no local pairs: every output row is zero
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < (size_t)T * H / 4;
@@ -437,6 +449,10 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
   }
 
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
+    // lane-dependent addresses are formed per unit (hoisted, they stay live across all paths)
+    int lane = lane_id();
+    asm volatile("" : "+v"(lane));
+    const int lr = lane & 15, kg = lane >> 4;
     const DecUnit du = decode_unit(u, S, NCB);
     const int4 mt = pl.mtiles[du.g];
     const int e = uniform(mt.x), row0 = uniform(mt.y), M = uniform(mt.z), flags = uniform(mt.w);
@@ -447,7 +463,66 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     const int prow = row0 + (lr < M ? lr : 0);
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 
-    if (!(flags & kFlagTwoTermC)) {
+    if (!(flags & kFlagTwoTermC) && M <= kPreRows && n <= kPre2MaxKB) {
+      const float swv = swp[min(lane, n - 1)];
+      v8i B[kDecDepth];
+      auto load = [&](int d, int j) { B[d] = load_v8i(bp + (size_t)min(j, n - 1) * kBlock); };
+#pragma unroll
+      for (int d = 0; d < kDecDepth; d++) load(d, d);
+      {
+        // rows [0, M) x K-blocks [kb0, kb0 + n) of C's hi term in 16-byte chunks (<= 4 per
+        // thread), then the M x n scales, all loads issued before the first store
+        constexpr int kChunksPerKB = kBlock * 2 / 16;
+        constexpr int kPer = kPreRows * kPre2MaxKB * kChunksPerKB / (64 * kDecBlockWaves);
+        const int nch = M * n * kChunksPerKB;
+        v4i v[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+          const int i = min((int)threadIdx.x + q * 64 * kDecBlockWaves, nch - 1);
+          const int r = i / (n * kChunksPerKB), c = i - r * n * kChunksPerKB;
+          v[q] = *reinterpret_cast<const v4i*>(ch.hi + (size_t)(row0 + r) * I + (size_t)kb0 * kBlock + c * 8);
+        }
+        const int si = min((int)threadIdx.x, M * n - 1), sr = si / n, sj = si - sr * n;
+        const float sv = ch.scale[(size_t)(row0 + sr) * KB + kb0 + sj];
+#pragma unroll
+        for (int q = 0; q < kPer; q++) {
+          const int i = threadIdx.x + q * 64 * kDecBlockWaves;
+          const int r = i / (n * kChunksPerKB), c = i - r * n * kChunksPerKB;
+          if (i < nch) *reinterpret_cast<v4i*>(sh.pre.a + r * kPre2RowBytes + c * 16) = v[q];
+        }
+        if ((int)threadIdx.x < M * n) sh.pre.sa[sj][sr] = sv;
+        __syncthreads();
+      }
+      // rows >= M read row M - 1 (real data, results discarded)
+      const uint8_t* arow = sh.pre.a + min(lr, M - 1) * kPre2RowBytes + kg * 64;
+      auto step = [&](int d, int j) {
+        v8h ah[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) ah[t] = *reinterpret_cast<const v8h*>(arow + j * (2 * kBlock) + t * 16);
+        const float4 sa = *reinterpret_cast<const float4*>(sh.pre.sa[j]);   // rows 0..3 (lanes kg = 0)
+        const float sw = readlane_f32(swv, j);
+        v8h b16[4];
+        widen_fp8_operand(B[d], b16);
+        const v4f p = mfma_f16_block(ah, b16, v4f{0.f, 0.f, 0.f, 0.f});
+        acc[0] += p[0] * (sa.x * sw);
+        acc[1] += p[1] * (sa.y * sw);
+        acc[2] += p[2] * (sa.z * sw);
+        acc[3] += p[3] * (sa.w * sw);
+      };
+      int j = 0;
+      for (; j + kDecDepth <= n; j += kDecDepth) {
+#pragma unroll
+        for (int d = 0; d < kDecDepth; d++) {
+          step(d, j + d);
+          load(d, j + d + kDecDepth);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < kDecDepth - 1; d++)
+        if (j + d < n) step(d, j + d);
+      __syncthreads();
+    } else if (!(flags & kFlagTwoTermC)) {
       // carriers: wave q loads rows 4q .. 4q + 3 of C's hi term as whole lines (lane l: row
       // 4q + l/16, 16-byte chunk l%16) and publishes them chunk-major; wave 0's lanes < 16 the
       // scale of row lane (all lanes load it: no loads under a branch)
