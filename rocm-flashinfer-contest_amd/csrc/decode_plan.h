@@ -29,6 +29,9 @@ struct DecodePlanScratch {
   int base[kEGlobal];                   // first pair row of each local expert
   int mtb[kEGlobal];                    // first m-tile of each local expert
   int ids[kSmallPairs];                 // local expert of each (token, k) pair, -1 if none
+  float w[kSmallPairs];                 // routing weight of each (token, k) pair
+  float a2[kSmallT];                    // squared hidden norm of each token
+  float esig[2 * kEGlobal];             // weight-scale estimates of each local expert
 };
 
 // K-split of a decode GEMM: the largest S in {8, 4, 2} whose units still fit the grid and
@@ -49,14 +52,18 @@ __device__ __forceinline__ int pick_split(int n_mt, int ncb, int kb, int slots, 
 __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, DecodePlanScratch& X, bool global) {
   const int tid = threadIdx.x, nth = blockDim.x, lane = lane_id(), wave = tid >> 6;
   const int T = a.T, E = a.E_local, NP = T * kTopK;
+  // every global input in one round of loads: ids, weights, token norms, expert estimates
   for (int e = tid; e < E; e += nth) X.tmask[e] = 0ull;
-  __syncthreads();
+  for (int i = tid; i < 2 * E; i += nth) X.esig[i] = a.esig[i];
+  for (int t = tid; t < T; t += nth) X.a2[t] = a.tok_a2[t];
   for (int i = tid; i < NP; i += nth) {
     const int le = a.topk_ids[i] - a.offset;
-    const bool local = le >= 0 && le < E;
-    X.ids[i] = local ? le : -1;
-    if (local) atomicOr(&X.tmask[le], 1ull << (i >> 3));
+    X.ids[i] = le >= 0 && le < E ? le : -1;
+    X.w[i] = a.topk_w[i];
   }
+  __syncthreads();
+  for (int i = tid; i < NP; i += nth)
+    if (X.ids[i] >= 0) atomicOr(&X.tmask[X.ids[i]], 1ull << (i >> 3));
   __syncthreads();
 
   // per-expert counts -> pair offsets, m-tile offsets, active list (wave 0, ballot prefix sums)
@@ -124,8 +131,8 @@ __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, Dec
     if (le >= 0) {
       const int pos = X.base[le] + (int)__popcll(X.tmask[le] & ((1ull << t) - 1ull));
       L.tok[pos] = t;
-      const float w = a.topk_w[i];
-      const float pred = predicted_output_rms(a.tok_a2[t], w, a.esig[2 * le], a.esig[2 * le + 1], a.sqrt_i);
+      const float w = X.w[i];
+      const float pred = predicted_output_rms(X.a2[t], w, X.esig[2 * le], X.esig[2 * le + 1], a.sqrt_i);
       const int flags = (pred > kPreciseRms ? kFlagExactProducts : 0) | (pred > kOneTermRms ? kFlagTwoTermC : 0);
       if (flags) atomicOr(&L.mt[X.mtb[le] + (pos - X.base[le]) / kSmallTile].w, flags);
       if (global) {

@@ -34,9 +34,9 @@ namespace moefp8 {
 
 constexpr int kDecBlockWaves = 4;            // wavefronts per workgroup = column groups per unit
 constexpr int kDec1BlocksPerCU = 5;          // GEMM1 resident workgroups per CU (<= 96 VGPRs)
-constexpr int kDec2BlocksPerCU = 4;          // GEMM2: its f16 operands need ~100 VGPRs (<= 128); at
-                                             // 5 per CU it spills, and the scratch traffic costs
-                                             // ~20% of its time (measured)
+constexpr int kDec2BlocksPerCU = 5;          // GEMM2 too (<= 96 VGPRs: its per-step path keeps a
+                                             // shallower ring; a scratch spill there cost ~20% of
+                                             // the kernel's time, measured)
 constexpr int kDecDepth = 3;                 // K-blocks in flight per wavefront (register ring)
 
 __device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
@@ -523,6 +523,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
         if (j + d < n) step(d, j + d);
       __syncthreads();
     } else if (!(flags & kFlagTwoTermC)) {
+      constexpr int kStepDepth2 = 2;   // (register budget shared with the staged path)
       // carriers: wave q loads rows 4q .. 4q + 3 of C's hi term as whole lines (lane l: row
       // 4q + l/16, 16-byte chunk l%16) and publishes them chunk-major; wave 0's lanes < 16 the
       // scale of row lane (all lanes load it: no loads under a branch)
@@ -530,9 +531,9 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       const _Float16* asrc = ch.hi + (size_t)(row0 + (ar < M ? ar : 0)) * I + (size_t)kb0 * kBlock + (lane & 15) * 8;
       const float* ssrc = ch.scale + (size_t)prow * KB + kb0;
       const float swv = swp[min(lane, n - 1)];
-      v8i B[kDecDepth];
-      v4i AR[kDecDepth];
-      float SR[kDecDepth];
+      v8i B[kStepDepth2];
+      v4i AR[kStepDepth2];
+      float SR[kStepDepth2];
       auto load = [&](int d, int j) {
         const int jj = min(j, n - 1);
         B[d] = load_v8i(bp + (size_t)jj * kBlock);
@@ -558,18 +559,18 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
         acc[3] += p[3] * (sa.w * sw);
       };
 #pragma unroll
-      for (int d = 0; d < kDecDepth; d++) load(d, d);
+      for (int d = 0; d < kStepDepth2; d++) load(d, d);
       int j = 0;
-      for (; j + kDecDepth <= n; j += kDecDepth) {
+      for (; j + kStepDepth2 <= n; j += kStepDepth2) {
 #pragma unroll
-        for (int d = 0; d < kDecDepth; d++) {
+        for (int d = 0; d < kStepDepth2; d++) {
           step(d, j + d);
-          load(d, j + d + kDecDepth);
+          load(d, j + d + kStepDepth2);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
 #pragma unroll
-      for (int d = 0; d < kDecDepth - 1; d++)
+      for (int d = 0; d < kStepDepth2 - 1; d++)
         if (j + d < n) step(d, j + d);
       __syncthreads();
     } else {
