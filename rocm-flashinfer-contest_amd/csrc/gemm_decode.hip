@@ -457,6 +457,8 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     G2Pre pre;
   } sh;
   __shared__ int last_s;
+  // per-wavefront weight transpose buffers of the staged path (16 rows x 128 bytes)
+  __shared__ __attribute__((aligned(16))) uint8_t wtr[kDecBlockWaves][16 * kBlock];
   G2Stage* ring = sh.ring;
   const int n_mt = pl.info[2], S = pl.info[4];
   const int H = pb.H, I = pb.I, T = pb.T;
@@ -488,8 +490,20 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
 
     if (!(flags & kFlagTwoTermC) && M <= kPreRows && n <= kPre2MaxKB) {
       const float swv = swp[min(lane, n - 1)];
-      v8i B[kDecDepth];
-      auto load = [&](int d, int j) { B[d] = load_v8i(bp + (size_t)min(j, n - 1) * kBlock); };
+      // weights as whole lines, transposed per wavefront through LDS (as in GEMM1)
+      const int wr = lane >> 3, wc = lane & 7;
+      const uint8_t* wsrc = pb.w2 + ((size_t)e * H + cg * 16 + wr) * I + (size_t)kb0 * kBlock + wc * 16;
+      uint8_t* const tb = wtr[wave];
+      uint8_t* const tw0 = tb + wr * kBlock + ((wc ^ (wr >> 1)) & 7) * 16;
+      uint8_t* const tw1 = tb + (wr + 8) * kBlock + ((wc ^ ((wr + 8) >> 1)) & 7) * 16;
+      const uint8_t* const trx = tb + lr * kBlock + (((2 * kg) ^ (lr >> 1)) & 7) * 16;
+      const uint8_t* const try_ = tb + lr * kBlock + (((2 * kg + 1) ^ (lr >> 1)) & 7) * 16;
+      v4i B0[kDecDepth], B1[kDecDepth];
+      auto load = [&](int d, int j) {
+        const uint8_t* p = wsrc + (size_t)min(j, n - 1) * kBlock;
+        B0[d] = *reinterpret_cast<const v4i*>(p);
+        B1[d] = *reinterpret_cast<const v4i*>(p + (size_t)8 * I);
+      };
 #pragma unroll
       for (int d = 0; d < kDecDepth; d++) load(d, d);
       {
@@ -519,13 +533,17 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       // rows >= M read row M - 1 (real data, results discarded)
       const uint8_t* arow = sh.pre.a + min(lr, M - 1) * kPre2RowBytes + kg * 64;
       auto step = [&](int d, int j) {
+        *reinterpret_cast<v4i*>(tw0) = B0[d];
+        *reinterpret_cast<v4i*>(tw1) = B1[d];
+        const v4i bx = *reinterpret_cast<const v4i*>(trx);
+        const v4i by = *reinterpret_cast<const v4i*>(try_);
         v8h ah[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) ah[t] = *reinterpret_cast<const v8h*>(arow + j * (2 * kBlock) + t * 16);
         const float4 sa = *reinterpret_cast<const float4*>(sh.pre.sa[j]);   // rows 0..3 (lanes kg = 0)
         const float sw = readlane_f32(swv, j);
         v8h b16[4];
-        widen_fp8_operand(B[d], b16);
+        widen_fp8_operand(__builtin_shufflevector(bx, by, 0, 1, 2, 3, 4, 5, 6, 7), b16);
         const v4f p = mfma_f16_block(ah, b16, v4f{0.f, 0.f, 0.f, 0.f});
         acc[0] += p[0] * (sa.x * sw);
         acc[1] += p[1] * (sa.y * sw);
