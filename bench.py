@@ -221,6 +221,31 @@ def cpu_baseline(wl, weights_cpu, threads):
                        f"all 32 experts dequantised up front as in the contest reference; {threads} threads")
 
 
+def measure_quantize(T, steps, flush, H=7168):
+    """Per-token 1x128 quantization of bf16 activations [T, H] (moe_fp8.quantize_hidden), cold
+    cache per call: bytes = T*H*2 read + T*H + T*H/128*4 written."""
+    import torch
+    import moe_fp8
+    g = torch.Generator(device="cuda").manual_seed(T)
+    x = torch.randn(T, H, generator=g, device="cuda").to(torch.bfloat16)
+    sink = torch.empty(1, dtype=torch.int64, device="cuda")
+    flush64 = flush.view(torch.int64)
+    for _ in range(3):
+        moe_fp8.quantize_hidden(x)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        torch.sum(flush64, dim=0, keepdim=True, out=sink)
+        starts[i].record()
+        moe_fp8.quantize_hidden(x)
+        ends[i].record()
+    torch.cuda.synchronize()
+    us = sorted(starts[i].elapsed_time(ends[i]) * 1e3 for i in range(steps))[steps // 2]
+    nbytes = T * H * 2 + T * H + T * (H // 128) * 4
+    return {"T": T, "us_per_call": round(us, 2), "bytes": nbytes, "gbps": round(nbytes / us / 1e3, 1),
+            "hbm_frac": round(nbytes / us / 1e3 / 8000.0, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -259,6 +284,11 @@ def main():
             print(f"# {name}: {r['us_per_call']:.1f} us/call", file=sys.stderr, flush=True)
             sweep[name] = r
     sec = sweep.get(args.secondary)
+    quant = None
+    if not args.no_sweep:
+        quant = {f"t{T}": measure_quantize(T, args.steps, flush) for T in (16, 8192)}
+        print(f"# quantize_hidden: T=16 {quant['t16']['us_per_call']} us, T=8192 {quant['t8192']['us_per_call']} us "
+              f"({quant['t8192']['hbm_frac']:.2f} of HBM)", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         threads = max(1, min(len(os.sched_getaffinity(0)), 16))
@@ -295,6 +325,8 @@ def main():
     if sec is not None:
         line["t8192"] = {k: sec[k] for k in ("us_per_call", "tflops", "gbps", "hbm_frac", "mfma_frac", "roofline_frac",
                                            "active_experts", "pairs", "stages_us", "roofline")}
+    if quant is not None:
+        line["quantize_hidden"] = quant
     if sweep:
         line["sweep"] = {k: {"us_per_call": round(v["us_per_call"], 2), "tflops": round(v["tflops"], 2),
                              "gbps": round(v["gbps"], 1), "roofline_frac": round(v["roofline_frac"], 4),

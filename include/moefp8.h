@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOEFP8_ABI_VERSION 2
+#define MOEFP8_ABI_VERSION 3
 
 /* Operator constants (solutions/moe_fp8/main.py:22-29). */
 #define MOEFP8_E_GLOBAL 256
@@ -125,6 +125,15 @@ int moefp8_run(const moefp8_args* args, void* workspace, size_t workspace_bytes,
 int moefp8_route(const void* routing_logits, int32_t logits_dtype, const void* routing_bias,
                  int32_t bias_dtype, int64_t num_tokens, float routed_scaling_factor,
                  int32_t* topk_ids, float* topk_weights, void* stream);
+
+/* Per-token 1x128 quantization of the hidden states, the step before the operator: produces
+ * the hidden_states / hidden_states_scale pair that moefp8_run reads (and that
+ * solutions/moe_fp8/main.py:129-136 dequantizes).  x [T, H] bf16 (x_dtype 1) or fp32 (0),
+ * row-major, 16-byte aligned; per token and 128 columns scale = amax / 448 (1 for an all-zero
+ * block), q = e4m3fn(x / scale) rounded to nearest even.  Writes hidden_out e4m3fn [T, H]
+ * (8-byte aligned) and scale_out fp32 [H/128, T].  Inputs must be finite. */
+int moefp8_quantize_hidden(const void* x, int32_t x_dtype, int64_t num_tokens, int32_t hidden_size,
+                           void* hidden_out, float* scale_out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,10 @@ reference solution ``solutions/moe_fp8/main.py`` of jhinpan/rocm-flashinfer-cont
 * ``swiglu``                         -- ``main.py:168-170`` (gate = second half).
 * ``moe_forward``                    -- ``run`` at ``main.py:173-243`` with fp32
   throughout (GEMM1, SwiGLU, GEMM2, ``index_add_`` combine, bf16 round).
+* ``quantize_hidden``                -- the step before the operator: the per-token
+  1x128 e4m3 quantization whose output ``main.py:129-136`` dequantizes (the reference
+  repository ships no quantizer; the convention is DeepSeek-V3's: scale = amax / 448,
+  1 for an all-zero block, q = e4m3fn(x / scale) rounded to nearest even).
 
 Canonical routing arithmetic.  ``torch.topk(sorted=False)`` leaves tie order
 and output order unspecified and ``weights.sum(dim=1)`` has an ISA-dependent
@@ -44,7 +48,11 @@ Pinning status (each item is checked in ``tests/test_oracle.py``):
                   (``tools/moe_parity.py:108-115``);
   moe_forward     dense fp64 formulation (every expert on every token, masked by
                   the dense routing weights) on reduced shapes, and golden
-                  fixtures produced by that formulation.
+                  fixtures produced by that formulation;
+  quantize_hidden codes vs a brute-force nearest-value encoder over the 256-code
+                  table with ties to the even code (so torch's cast is checked,
+                  not trusted), scales vs the closed form, round trip of every
+                  finite code, the block maximum landing on +-448.
   torch's own sigmoid ulp / sum association / topk tie bits are not pinned
   (the contest's torch reference is not available offline); the canonical
   form above replaces them.
@@ -113,6 +121,39 @@ def dequant_hidden(hidden_codes, hidden_scale) -> torch.Tensor:
     T, H = q.shape
     assert sc.shape == (H // BLOCK, T), (sc.shape, H, T)
     return (q.view(T, H // BLOCK, BLOCK) * sc.t().unsqueeze(-1)).reshape(T, H)
+
+
+def quantize_hidden(x):
+    """Per-token 1x128 quantization of ``x [T, H]`` (any float dtype, finite):
+    returns ``(codes uint8 [T, H], scale fp32 [H/128, T])`` with, per token and
+    128 columns, ``scale = fp32(amax / 448)`` (1 for an all-zero block) and
+    ``codes = e4m3fn(fp32(x / scale))`` rounded to nearest even -- the pair that
+    ``dequant_hidden`` (``main.py:129-136``) turns back into activations."""
+    x32 = torch.as_tensor(x).detach().cpu().float()
+    T, H = x32.shape
+    xb = x32.view(T, H // BLOCK, BLOCK)
+    amax = xb.abs().amax(dim=2)
+    scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    codes = (xb / scale.unsqueeze(-1)).to(torch.float8_e4m3fn).view(torch.uint8).reshape(T, H)
+    return codes.numpy(), scale.t().contiguous().numpy()
+
+
+def encode_e4m3_bruteforce(v) -> np.ndarray:
+    """Reference encoder for the tests: for each finite fp32 value with |v| <= 464,
+    the non-negative e4m3fn code whose value is nearest to |v| (ties to the even
+    mantissa, i.e. round to nearest even), with the sign bit of v -- straight from
+    the 256-code table."""
+    v = np.asarray(v, dtype=np.float64).reshape(-1)
+    mags = np.arange(0x7F, dtype=np.int64)            # codes 0x00..0x7E (0x7F is NaN)
+    vals = E4M3_TABLE[mags].astype(np.float64)
+    out = np.empty(v.shape, dtype=np.uint8)
+    for i, x in enumerate(v):
+        d = np.abs(vals - abs(x))
+        cand = mags[d == d.min()]
+        if len(cand) > 1:
+            cand = cand[(cand & 1) == 0]
+        out[i] = int(cand[0]) | (0x80 if math.copysign(1.0, x) < 0 else 0)
+    return out
 
 
 def dequant_block(w_codes, scale) -> torch.Tensor:

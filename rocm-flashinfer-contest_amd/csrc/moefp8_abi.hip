@@ -220,6 +220,21 @@ int moefp8_route(const void* routing_logits, int32_t logits_dtype, const void* r
   return hipGetLastError() == hipSuccess ? MOEFP8_OK : MOEFP8_ERR_LAUNCH;
 }
 
+int moefp8_quantize_hidden(const void* x, int32_t x_dtype, int64_t num_tokens, int32_t hidden_size,
+                           void* hidden_out, float* scale_out, void* stream) {
+  if (num_tokens < 0 || num_tokens > (int64_t)1 << 24) return MOEFP8_ERR_SHAPE;
+  if (hidden_size <= 0 || hidden_size % kBlock != 0) return MOEFP8_ERR_SHAPE;
+  if (x_dtype != 0 && x_dtype != 1) return MOEFP8_ERR_DTYPE;
+  if (num_tokens == 0) return MOEFP8_OK;
+  if (!x || !hidden_out || !scale_out) return MOEFP8_ERR_NULL_POINTER;
+  if (!aligned16(x) || ((uintptr_t)hidden_out & 7u) || ((uintptr_t)scale_out & 3u)) return MOEFP8_ERR_ALIGNMENT;
+  int dev;
+  if (query_device(&dev)) return MOEFP8_ERR_DEVICE;
+  launch_quantize_hidden(x, x_dtype, num_tokens, hidden_size, reinterpret_cast<uint8_t*>(hidden_out), scale_out,
+                         (hipStream_t)stream);
+  return hipGetLastError() == hipSuccess ? MOEFP8_OK : MOEFP8_ERR_LAUNCH;
+}
+
 int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, void* stream) {
   if (!a) return MOEFP8_ERR_NULL_POINTER;
   const int64_t T = a->num_tokens;

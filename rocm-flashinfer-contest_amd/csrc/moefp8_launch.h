@@ -148,6 +148,10 @@ void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float
 
 void launch_combine(const Plan& pl, const float* obuf, uint16_t* out, int T, int H, hipStream_t stream);
 
+// Per-token 1x128 e4m3 quantization of bf16 (x_dt 1) or fp32 (0) activations [T, H] into
+// q [T, H] and scale [H/128, T].
+void launch_quantize_hidden(const void* x, int x_dt, int64_t T, int H, uint8_t* q, float* scale, hipStream_t stream);
+
 int num_compute_units();
 
 }  // namespace moefp8

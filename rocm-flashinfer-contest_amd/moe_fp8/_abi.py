@@ -12,7 +12,7 @@ from pathlib import Path
 LIB_NAME = "libmoefp8.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -30,7 +30,8 @@ STATUS = {
 }
 
 # Every extern "C" symbol of include/moefp8.h.
-EXPORTS = ("moefp8_abi_version", "moefp8_strerror", "moefp8_workspace_size", "moefp8_run", "moefp8_route")
+EXPORTS = ("moefp8_abi_version", "moefp8_strerror", "moefp8_workspace_size", "moefp8_run", "moefp8_route",
+           "moefp8_quantize_hidden")
 
 
 class MoeFp8Args(ctypes.Structure):
@@ -97,6 +98,9 @@ def load(path: os.PathLike | None = None):
     lib.moefp8_route.restype = ctypes.c_int
     lib.moefp8_route.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
                                  ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.moefp8_quantize_hidden.restype = ctypes.c_int
+    lib.moefp8_quantize_hidden.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_int32,
+                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
     if lib.moefp8_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{p}: ABI version {lib.moefp8_abi_version()} != {ABI_VERSION}")
     if path is None:

@@ -216,3 +216,28 @@ def route(routing_logits, routing_bias, routed_scaling_factor):
                                          _scalar(routed_scaling_factor, float), ids.data_ptr(), w.data_ptr(),
                                          stream))
     return ids, w
+
+
+def quantize_hidden(x):
+    """Per-token 1x128 quantization of activations ``x [T, H]`` (bf16 or fp32, device
+    tensor, H a multiple of 128): returns ``(hidden_states e4m3fn [T, H],
+    hidden_states_scale fp32 [H/128, T])``, the pair ``run`` consumes and
+    ``main.py:129-136`` dequantizes, with scale = amax / 448 per token and 128 columns
+    (1 for an all-zero block) and q = e4m3(x / scale) rounded to nearest even."""
+    lib = _abi.load()
+    device = x.device
+    if device.type != "cuda":
+        raise ValueError("x must be a device (cuda/HIP) tensor")
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"x must be bfloat16 or float32, got {x.dtype}")
+    if x.dim() != 2 or x.shape[1] % BLOCK != 0:
+        raise ValueError(f"x must be [T, H] with H a multiple of {BLOCK}, got {tuple(x.shape)}")
+    x = x.contiguous()
+    T, Hd = int(x.shape[0]), int(x.shape[1])
+    q = torch.empty((T, Hd), dtype=torch.float8_e4m3fn, device=device)
+    scale = torch.empty((Hd // BLOCK, T), dtype=torch.float32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    with torch.cuda.device(device):
+        _abi.check(lib, lib.moefp8_quantize_hidden(x.data_ptr(), _DT[x.dtype], T, Hd, q.data_ptr(), scale.data_ptr(),
+                                                   stream))
+    return q, scale

@@ -116,6 +116,10 @@ REDUCED = [
     (50, 32, 256, 128, 300),
     (2500, 32, 256, 128, 0),
     (2100, 16, 512, 256, 0),        # 128-row blocks with 4 K-blocks
+    (16, 32, 512, 256, 32),         # expert-parallel rank 1 (one routing group)
+    (40, 32, 256, 128, 240),        # rank owning experts 240..271: half past the last expert
+    (500, 32, 256, 128, 32),
+    (300, 32, 512, 256, 240),
 ]
 
 
