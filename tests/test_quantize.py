@@ -29,6 +29,35 @@ def sample(T, H, seed, dtype=torch.float32):
     return x.to(dtype)
 
 
+def hard_scales(T, H, seed, dtype=torch.float32):
+    """Blocks whose scales stress the division: block maxima with all-ones mantissas, exact
+    powers of two, values just above/below them, tiny (near the fp32 normal minimum) and
+    huge magnitudes, each block filled with random multiples of the maximum."""
+    g = torch.Generator().manual_seed(seed)
+    nb = H // 128
+    maxes = []
+    for k in range(T * nb):
+        kind = k % 6
+        e = int(torch.randint(-60, 60, (1,), generator=g))
+        if kind == 0:
+            m = (2.0 - 2.0**-23) * 2.0**e            # all-ones mantissa
+        elif kind == 1:
+            m = 2.0**e
+        elif kind == 2:
+            m = 2.0**e * (1 + 2.0**-23)
+        elif kind == 3:
+            m = 2.0**e * (1 - 2.0**-24)
+        elif kind == 4:
+            m = 2.0**-120 * float(torch.rand(1, generator=g) + 1)   # scale below 2^-100 (slow path)
+        else:
+            m = float(torch.rand(1, generator=g) + 0.5) * 2.0**int(torch.randint(-30, 30, (1,), generator=g))
+        maxes.append(m)
+    mx = torch.tensor(maxes, dtype=torch.float64).view(T, nb, 1)
+    frac = torch.rand(T, nb, 128, generator=g, dtype=torch.float64) * 2 - 1
+    frac[:, :, 0] = 1.0
+    return (frac * mx).view(T, H).to(torch.float32).to(dtype)
+
+
 # ------------------------------------------------------------------------------------------ CPU: oracle
 
 
@@ -93,6 +122,20 @@ def test_quantize_bitexact(T, H, dtype):
     assert tuple(scale.shape) == (H // 128, T)
     assert np.array_equal(scale.cpu().numpy(), want_scale)
     assert np.array_equal(q.view(torch.uint8).cpu().numpy(), want_codes)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_quantize_hard_scales(dtype):
+    import moe_fp8
+    print(f"[quantize] hard scales {dtype}", flush=True)
+    x = hard_scales(512, 1024, 21, dtype)
+    q, scale = moe_fp8.quantize_hidden(x.to(DEV))
+    torch.cuda.synchronize()
+    want_codes, want_scale = O.quantize_hidden(x)
+    assert np.array_equal(scale.cpu().numpy(), want_scale)
+    got = q.view(torch.uint8).cpu().numpy()
+    assert np.array_equal(got, want_codes), f"{int((got != want_codes).sum())} codes differ"
 
 
 @pytest.mark.gpu
