@@ -10,7 +10,7 @@
 #include <atomic>
 #include <cstring>
 
-#include "../../include/moefp8.h"
+#include "moefp8.h"
 #include "moefp8_device.h"
 #include "moefp8_launch.h"
 

@@ -13,6 +13,7 @@ from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR.parent / "csrc"
+INCLUDE = PKG_DIR.parent.parent / "include"
 LIB = PKG_DIR / "libmoefp8.so"
 ARCH = "gfx950"
 
@@ -42,7 +43,7 @@ def build(verbose: bool = False) -> Path:
         objs, procs = [], []
         for s in srcs:
             o = Path(tmp) / (s.stem + ".o")
-            cmd = [cc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)]
+            cmd = [cc, *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(s), "-o", str(o)]
             if verbose:
                 print(" ".join(cmd), flush=True)
             procs.append((s, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
