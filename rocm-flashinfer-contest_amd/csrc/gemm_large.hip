@@ -144,6 +144,49 @@ __device__ __forceinline__ v4f mfma16x16x128_exp(const v8i& a, const v8i& b, con
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, kExp, 0, 127);
 }
 
+// ------------------------------------------------------------------------------------------ units
+// Units (m-block, column block) are ordered expert by expert, then column block by column block,
+// the expert's m-blocks innermost.  Workgroup b of a grid that is a multiple of 8 runs on XCD b % 8
+// (workgroups are dispatched to the XCDs round robin), and XCD x takes the x-th eighth of that
+// order, its workgroups stepping through it together: the units that run at the same time on one
+// XCD then share their expert's weight column blocks and activation blocks through that XCD's L2
+// instead of each XCD fetching them from HBM.
+struct UnitWalk {
+  int v, end, step;
+};
+__device__ __forceinline__ UnitWalk unit_walk(int n_units) {
+  const int nx = gridDim.x % 8 == 0 ? 8 : 1;
+  const int x = blockIdx.x % nx;
+  const int lo = (int)((int64_t)n_units * x / nx), hi = (int)((int64_t)n_units * (x + 1) / nx);
+  return UnitWalk{lo + (int)blockIdx.x / nx, hi, (int)gridDim.x / nx};
+}
+// The 128-row kernels take their units from per-XCD queues over the same eighths (queue[x] counts
+// the units of eighth x handed out), in order, and a workgroup whose eighth is used up takes units
+// from the other eighths: unit costs differ (block heights, precision modes), and a static split
+// would leave some XCDs idle at the end.  Thread 0 grabs; -1 when every eighth is used up.
+__device__ __forceinline__ int grab_unit(int* queues, int n_units) {
+  const int nx = gridDim.x % 8 == 0 ? 8 : 1;
+  const int x = blockIdx.x % nx;
+  for (int d = 0; d < nx; d++) {
+    const int y = (x + d) % nx;
+    const int lo = (int)((int64_t)n_units * y / nx), hi = (int)((int64_t)n_units * (y + 1) / nx);
+    if (lo >= hi) continue;
+    // a relaxed load first, so that a used-up eighth costs no atomic
+    if (__hip_atomic_load(queues + y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= hi - lo) continue;
+    const int k = __hip_atomic_fetch_add(queues + y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (k < hi - lo) return lo + k;
+  }
+  return -1;
+}
+
+// Unit v of that order as {m-block, column block}; mbgroup[g] = {first m-block of g's expert,
+// the expert's m-blocks}, so the units of an expert are [first * NC, (first + count) * NC).
+__device__ __forceinline__ int2 unit_at(const int2* mbgroup, int v, int NC) {
+  const int2 g = mbgroup[v / NC];
+  const int local = v - g.x * NC;
+  return int2{g.x + local % g.y, local / g.y};
+}
+
 // ------------------------------------------------------------------------------------------ GEMM1
 // LDS stage: MT m-tiles x [8 chunks of 16 B][16 rows][16 B] of e4m3 activations, then 4 x 64
 // row scales (one slot per wavefront; rows >= BM are padding).
@@ -342,10 +385,10 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, 
   __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
   __shared__ float amax_s[kLgWaves][16 * MT];
   const int I = pb.I, NCB = I / kBlock;
-  const int n_units = pl.info[2] * NCB;
-
-  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-    const int mb = u / NCB, cb = u % NCB;
+  const UnitWalk w = unit_walk(pl.info[2] * NCB);
+  for (int v = w.v; v < w.end; v += w.step) {
+    const int2 uc = unit_at(pl.mbgroup1, v, NCB);
+    const int mb = uniform(uc.x), cb = uniform(uc.y);
     const int4 blk = pl.mblocks1[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
     const int mvalid = (rows + 15) / 16;
@@ -397,13 +440,16 @@ constexpr int kBgOps = 2 + 4 + 1;            // per wavefront and K-block: A, B 
 
 __device__ __forceinline__ int bg_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-// One unit.  kExact (blocks of at most 32 exact-product rows): wavefront (wm, wn) takes m-tile wm
-// alone, on the f16 MFMA with operands widened exactly, and C's lo term is written in f16.
-template <bool kExact>
+// One unit.  Wavefront (wm, wn) computes m-tiles NT wm .. NT wm + NT - 1: NT = 4 for blocks of more
+// than 64 rows, 2 for 33..64 rows and 1 for at most 32 (the short last blocks of an expert's
+// classes cost a quarter of the MFMA and VALU work of a full one).  kExact (blocks of at most 32
+// exact-product rows, NT = 1): the f16 MFMA on operands widened exactly, and C's lo term in f16.
+template <int NT, bool kExact>
 __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float2* sw_s, float (*amax_s)[kBgRows],
                                                int e, int row0, int rows, int cb, int flags) {
-  constexpr int NT = kExact ? 1 : 4;    // m-tiles per wavefront
+  static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
+  static_assert(!kExact || NT == 1, "exact-product blocks hold at most 32 rows");
   const int H = pb.H, I = pb.I, T = pb.T, KB = H / kBlock, NCB = I / kBlock;
   const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
@@ -470,7 +516,7 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
     const float2 sw = sw_s[j];
 #pragma unroll
     for (int i = 0; i < NT; i++) {
-      const int t = kExact ? wm : 4 * wm + i;
+      const int t = NT * wm + i;
       const uint8_t* at = st + t * 16 * 128;
       const v8i a = cat(*reinterpret_cast<const v4i*>(at + rd0), *reinterpret_cast<const v4i*>(at + rd1));
       const float4 sa = *reinterpret_cast<const float4*>(st + kBgA + kBgB + (16 * t + 4 * kg) * 4);
@@ -511,7 +557,7 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
       for (int r = 0; r < 4; r++) c[i][jn][r] = silu_f32(acc[i][jn + 2][r]) * acc[i][jn][r];
 #pragma unroll
   for (int i = 0; i < NT; i++) {
-    const int t = kExact ? wm : 4 * wm + i;
+    const int t = NT * wm + i;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       float m = fmaxf(fabsf(c[i][0][r]), fabsf(c[i][1][r]));
@@ -526,7 +572,7 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
   const bool two = (flags & kFlagTwoTermC) != 0;
 #pragma unroll
   for (int i = 0; i < NT; i++) {
-    const int t = kExact ? wm : 4 * wm + i;
+    const int t = NT * wm + i;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int row = 16 * t + 4 * kg + r;
@@ -557,26 +603,36 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Pl
   __shared__ __attribute__((aligned(16))) float2 sw_s[kBigMaxKB];
   __shared__ float amax_s[4][kBgRows];
   const int H = pb.H, I = pb.I, KB = H / kBlock, NCB = I / kBlock;
-  const int n_units = pl.info[2] * NCB;
+  __shared__ int next_s;
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
-  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-    const int mb = u / NCB, cb = u % NCB;
+  const int n_units = pl.info[2] * NCB;
+  if (threadIdx.x == 0) next_s = grab_unit(pl.queues, n_units);
+  __syncthreads();
+  for (int v = uniform(next_s); v >= 0; v = uniform(next_s)) {
+    const int2 uc = unit_at(pl.mbgroup1, v, NCB);
+    const int mb = uniform(uc.x), cb = uniform(uc.y);
     const int4 blk = pl.mblocks1[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
-    // the previous unit's readers are done with the ring, amax_s and sw_s
+    // the previous unit's readers are done with the ring, amax_s and sw_s, and every thread has
+    // read next_s
     __syncthreads();
-    // weight scales of the unit: {up, gate} per K-block
+    // weight scales of the unit: {up, gate} per K-block; the next unit
     {
       const float* su = pb.s13 + ((size_t)e * (2 * I / kBlock) + cb) * KB;
       const float* sg = su + (size_t)NCB * KB;
       const int t = threadIdx.x;
       if (t < KB) sw_s[t] = float2{su[t], sg[t]};
+      if (t == 0) next_s = grab_unit(pl.queues, n_units);
     }
     __syncthreads();
     if (flags & kFlagExactProducts)
-      gemm1_big_unit<true>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
+      gemm1_big_unit<1, true>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
+    else if (rows <= 32)
+      gemm1_big_unit<1, false>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
+    else if (rows <= 64)
+      gemm1_big_unit<2, false>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
     else
-      gemm1_big_unit<false>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
+      gemm1_big_unit<4, false>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
   }
 }
 
@@ -762,9 +818,10 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
   constexpr int NP = MT / 2;
   __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
   const int H = pb.H, HB = H / kBlock;
-  const int n_units = pl.info[5] * HB;
-  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-    const int mb = u / HB, hb = u % HB;
+  const UnitWalk w = unit_walk(pl.info[5] * HB);
+  for (int v = w.v; v < w.end; v += w.step) {
+    const int2 uc = unit_at(pl.mbgroup2, v, HB);
+    const int mb = uniform(uc.x), hb = uniform(uc.y);
     const int4 blk = pl.mblocks2[mb];
     const int e = uniform(blk.x), flags = uniform(blk.w);
     for (int s0 = 0; s0 < blk.z; s0 += 16 * MT) {
@@ -832,14 +889,16 @@ __device__ __forceinline__ void widen16(const v4i& x, float scale, v8h& t0, v8h&
   }
 }
 
-// One unit.  kMode: kOneTerm / kTwoTerms (128-row blocks, 4 m-tiles per wavefront), kPrecise
-// (blocks of at most 32 exact-product rows: wavefront (wm, wn) takes m-tile wm with C's hi and
-// f16 lo terms, the lo rows staged in the stage's lo region as [32 rows][128 B]).
-template <int kMode>
+// One unit.  Wavefront (wm, wn) computes m-tiles NT wm .. NT wm + NT - 1 (NT = 4, 2 or 1 for
+// blocks of more than 64, 33..64 and at most 32 rows).  kMode: kOneTerm / kTwoTerms, kPrecise
+// (blocks of at most 32 exact-product rows, NT = 1, with C's hi and f16 lo terms, the lo rows
+// staged in the stage's lo region as [32 rows][128 B]).
+template <int kMode, int NT>
 __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float* sw2_s, int e, int row0, int rows,
                                                int hc, float* __restrict__ obuf) {
-  constexpr int NT = kMode == kPrecise ? 1 : 4;
+  static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
+  static_assert(kMode != kPrecise || NT == 1, "exact-product blocks hold at most 32 rows");
   const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
   const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
@@ -910,7 +969,7 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
     const float sw = sw2_s[(j / 2) * 2 + (wn >> 1)];
 #pragma unroll
     for (int i = 0; i < NT; i++) {
-      const int t = kMode == kPrecise ? wm : 4 * wm + i;
+      const int t = NT * wm + i;
       const uint8_t* ht = st + t * 16 * 128;
       const v8h a0 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh0));
       const v8h a1 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh1));
@@ -943,7 +1002,7 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
   MOEFP8_WAIT_VMCNT(0);
 #pragma unroll
   for (int i = 0; i < NT; i++) {
-    const int t = kMode == kPrecise ? wm : 4 * wm + i;
+    const int t = NT * wm + i;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int row = 16 * t + 4 * kg + r;
@@ -963,26 +1022,37 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
   __shared__ __attribute__((aligned(16))) uint8_t ring[kB2Stages * kB2Stage];
   __shared__ float sw2_s[2 * kBigMaxKB];
   const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock, HC = H / kB2Cols;
-  const int n_units = pl.info[5] * HC;
+  __shared__ int next_s;
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
-  for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
-    const int mb = u / HC, hc = u % HC;
+  const int n_units = pl.info[5] * HC;
+  int* queues = pl.queues + 8;
+  if (threadIdx.x == 0) next_s = grab_unit(queues, n_units);
+  __syncthreads();
+  for (int v = uniform(next_s); v >= 0; v = uniform(next_s)) {
+    const int2 uc = unit_at(pl.mbgroup2, v, HC);
+    const int mb = uniform(uc.x), hc = uniform(uc.y);
     const int4 blk = pl.mblocks2[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
-    // the previous unit's readers are done with the ring and sw2_s
+    // the previous unit's readers are done with the ring and sw2_s, and every thread has read next_s
     __syncthreads();
-    // W2 block scales of the unit's two 128-column blocks, per 128-K block
+    // W2 block scales of the unit's two 128-column blocks, per 128-K block; the next unit
     {
       const int t = threadIdx.x;
       if (t < 2 * KB) sw2_s[t] = pb.s2[((size_t)e * HB + 2 * hc + (t & 1)) * KB + (t >> 1)];
+      if (t == 0) next_s = grab_unit(queues, n_units);
     }
     __syncthreads();
     if (flags & kFlagExactProducts)
-      gemm2_big_unit<kPrecise>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
-    else if (flags & kFlagTwoTermC)
-      gemm2_big_unit<kTwoTerms>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
-    else
-      gemm2_big_unit<kOneTerm>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+      gemm2_big_unit<kPrecise, 1>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+    else if (flags & kFlagTwoTermC) {
+      if (rows <= 32) gemm2_big_unit<kTwoTerms, 1>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+      else if (rows <= 64) gemm2_big_unit<kTwoTerms, 2>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+      else gemm2_big_unit<kTwoTerms, 4>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+    } else {
+      if (rows <= 32) gemm2_big_unit<kOneTerm, 1>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+      else if (rows <= 64) gemm2_big_unit<kOneTerm, 2>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+      else gemm2_big_unit<kOneTerm, 4>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+    }
   }
 }
 

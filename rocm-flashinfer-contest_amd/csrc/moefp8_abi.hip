@@ -37,7 +37,7 @@ int large_rows_b(int64_t T, int H, int I) { return large_big(T, H, I) ? kExactRo
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
   size_t tok_a2, esig, mtiles, counters, c16, c16_scale, gbuf, obuf;
-  size_t canon_token, bcnt, ccnt, mblocks1, mblocks2, c_hi, c_lo, c_lo16, c_scale;
+  size_t canon_token, bcnt, ccnt, mblocks1, mblocks2, mbgroup1, mbgroup2, queues, c_hi, c_lo, c_lo16, c_scale;
   size_t total;
   int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks1, max_blocks2, n_counters1, n_counters;
   int nblk;
@@ -102,6 +102,9 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.ccnt = take((size_t)L.nblk * E_local * 4);
   L.mblocks1 = take((size_t)L.max_blocks1 * 16);
   L.mblocks2 = take((size_t)L.max_blocks2 * 16);
+  L.mbgroup1 = take((size_t)L.max_blocks1 * 8);
+  L.mbgroup2 = take((size_t)L.max_blocks2 * 8);
+  L.queues = take((size_t)kUnitQueues * 4);
   L.c_hi = take((size_t)pmax * I * 2);
   L.c_lo = take((size_t)pmax * I);
   L.c_lo16 = take((size_t)pmax * I * 2);
@@ -274,6 +277,9 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pl.mtiles = nullptr;
   pl.mblocks1 = nullptr;
   pl.mblocks2 = nullptr;
+  pl.mbgroup1 = nullptr;
+  pl.mbgroup2 = nullptr;
+  pl.queues = nullptr;
   pl.canon_token = pl.perm_token;
   pl.counters = nullptr;
   pl.counters2 = nullptr;
@@ -366,11 +372,17 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pa.tok_slot = const_cast<int*>(pl.tok_slot);
   pa.mblocks1 = reinterpret_cast<int4*>(ws + L.mblocks1);
   pa.mblocks2 = reinterpret_cast<int4*>(ws + L.mblocks2);
+  pa.mbgroup1 = reinterpret_cast<int2*>(ws + L.mbgroup1);
+  pa.mbgroup2 = reinterpret_cast<int2*>(ws + L.mbgroup2);
+  pa.queues = reinterpret_cast<int*>(ws + L.queues);
   pa.rows_a = large_rows_a(T, H, I);
   pa.rows_b = large_rows_b(T, H, I);
   pl.canon_token = pa.canon_token;
   pl.mblocks1 = pa.mblocks1;
   pl.mblocks2 = pa.mblocks2;
+  pl.mbgroup1 = pa.mbgroup1;
+  pl.mbgroup2 = pa.mbgroup2;
+  pl.queues = pa.queues;
   CHalf8 ch;
   ch.hi = reinterpret_cast<_Float16*>(ws + L.c_hi);
   ch.lo = ws + L.c_lo;

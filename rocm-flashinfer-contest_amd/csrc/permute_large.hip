@@ -90,6 +90,7 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
   __shared__ int tot[kEGlobal * kClasses];
   __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], eb1[kEGlobal + 1], eb2[kEGlobal + 1];
   const int E = a.E_local, E3 = E * kClasses, nb = a.nblk, tid = threadIdx.x, lane = lane_id();
+  if (tid < kUnitQueues) a.queues[tid] = 0;
 
   // canonical per-block base of each expert (relative), from the raw counts
   for (int e = tid; e < E; e += kScanThreads) {
@@ -182,6 +183,7 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
       const int r0 = c01 + (j - ba) * a.rows_b;
       a.mblocks1[g] = int4{e, eoff[e] + r0, min(a.rows_b, n - r0), (int)class_flags(2)};
     }
+    a.mbgroup1[g] = int2{eb1[e], eb1[e + 1] - eb1[e]};
   }
   for (int g = tid; g < eb2[E]; g += kScanThreads) {
     const int e = upper_bound(eb2, E + 1, g) - 1, j = g - eb2[e];
@@ -197,6 +199,7 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
       const int r0 = c01 + (j - b01) * a.rows_b;
       a.mblocks2[g] = int4{e, eoff[e] + r0, min(a.rows_b, n - r0), (int)class_flags(2)};
     }
+    a.mbgroup2[g] = int2{eb2[e], eb2[e + 1] - eb2[e]};
   }
 }
 
