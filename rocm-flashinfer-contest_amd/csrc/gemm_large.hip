@@ -146,37 +146,45 @@ __device__ __forceinline__ v4f mfma16x16x128_exp(const v8i& a, const v8i& b, con
 
 // ------------------------------------------------------------------------------------------ units
 // Units (m-block, column block) are ordered expert by expert, then column block by column block,
-// the expert's m-blocks innermost.  Workgroup b of a grid that is a multiple of 8 runs on XCD b % 8
-// (workgroups are dispatched to the XCDs round robin), and XCD x takes the x-th eighth of that
-// order, its workgroups stepping through it together: the units that run at the same time on one
-// XCD then share their expert's weight column blocks and activation blocks through that XCD's L2
-// instead of each XCD fetching them from HBM.
-struct UnitWalk {
-  int v, end, step;
-};
-__device__ __forceinline__ UnitWalk unit_walk(int n_units) {
-  const int nx = gridDim.x % 8 == 0 ? 8 : 1;
-  const int x = blockIdx.x % nx;
-  const int lo = (int)((int64_t)n_units * x / nx), hi = (int)((int64_t)n_units * (x + 1) / nx);
-  return UnitWalk{lo + (int)blockIdx.x / nx, hi, (int)gridDim.x / nx};
-}
-// The 128-row kernels take their units from per-XCD queues over the same eighths (queue[x] counts
-// the units of eighth x handed out), in order, and a workgroup whose eighth is used up takes units
+// the expert's m-blocks innermost, and the order is cut into eighths.  Workgroup b of a grid that
+// is a multiple of 8 runs on XCD b % 8 (workgroups are dispatched to the XCDs round robin) and works
+// through eighth b % 8 with the other workgroups of its XCD, in order: the units that run at the
+// same time on one XCD share their expert's weight column blocks and activation blocks through that
+// XCD's L2 instead of each XCD fetching them from HBM.  Its first unit is eighth[b / 8]; later ones
+// come from a per-XCD queue (queue x counts the units of eighth x handed out past the first
+// round), claimed when the workgroup is free, and a workgroup whose eighth is used up takes units
 // from the other eighths: unit costs differ (block heights, precision modes), and a static split
-// would leave some XCDs idle at the end.  Thread 0 grabs; -1 when every eighth is used up.
+// would leave XCDs idle at the end.  The counters sit on separate 256-byte lines.  The smaller-T
+// kernels (about one unit per workgroup) keep the static split: workgroup b takes units
+// eighth[b / 8], eighth[b / 8 + grid / 8], ... (measured faster there than claiming).
+struct UnitEighths {
+  int nx, x, per;
+  __device__ __forceinline__ UnitEighths() {
+    nx = gridDim.x % 8 == 0 ? 8 : 1;
+    x = blockIdx.x % nx;
+    per = gridDim.x / nx;
+  }
+  __device__ __forceinline__ int lo(int n_units, int y) const { return (int)((int64_t)n_units * y / nx); }
+};
+// Thread 0 claims; -1 when every eighth is used up.
 __device__ __forceinline__ int grab_unit(int* queues, int n_units) {
-  const int nx = gridDim.x % 8 == 0 ? 8 : 1;
-  const int x = blockIdx.x % nx;
-  for (int d = 0; d < nx; d++) {
-    const int y = (x + d) % nx;
-    const int lo = (int)((int64_t)n_units * y / nx), hi = (int)((int64_t)n_units * (y + 1) / nx);
-    if (lo >= hi) continue;
+  const UnitEighths u;
+  for (int d = 0; d < u.nx; d++) {
+    const int y = (u.x + d) % u.nx;
+    const int lo = u.lo(n_units, y), n = u.lo(n_units, y + 1) - lo;
+    int* q = queues + y * kQueueStride;
     // a relaxed load first, so that a used-up eighth costs no atomic
-    if (__hip_atomic_load(queues + y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= hi - lo) continue;
-    const int k = __hip_atomic_fetch_add(queues + y, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (k < hi - lo) return lo + k;
+    if (u.per + __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= n) continue;
+    const int k = u.per + __hip_atomic_fetch_add(q, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (k < n) return lo + k;
   }
   return -1;
+}
+
+__device__ __forceinline__ int first_unit(int* queues, int n_units) {
+  const UnitEighths u;
+  const int v = u.lo(n_units, u.x) + (int)blockIdx.x / u.nx;
+  return v < u.lo(n_units, u.x + 1) ? v : grab_unit(queues, n_units);
 }
 
 // Unit v of that order as {m-block, column block}; mbgroup[g] = {first m-block of g's expert,
@@ -385,8 +393,9 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, 
   __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
   __shared__ float amax_s[kLgWaves][16 * MT];
   const int I = pb.I, NCB = I / kBlock;
-  const UnitWalk w = unit_walk(pl.info[2] * NCB);
-  for (int v = w.v; v < w.end; v += w.step) {
+  const UnitEighths u;
+  const int n_units = pl.info[2] * NCB, end = u.lo(n_units, u.x + 1);
+  for (int v = u.lo(n_units, u.x) + (int)blockIdx.x / u.nx; v < end; v += u.per) {
     const int2 uc = unit_at(pl.mbgroup1, v, NCB);
     const int mb = uniform(uc.x), cb = uniform(uc.y);
     const int4 blk = pl.mblocks1[mb];
@@ -447,7 +456,8 @@ __device__ __forceinline__ int bg_key(int row) { return (row & 7) ^ ((row >> 3) 
 template <int NT, bool kExact>
 __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float2* sw_s, float (*amax_s)[kBgRows],
-                                               int e, int row0, int rows, int cb, int flags) {
+                                               int e, int row0, int rows, int cb, int flags, int* next_s,
+                                               int n_units) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
   static_assert(!kExact || NT == 1, "exact-product blocks hold at most 32 rows");
   const int H = pb.H, I = pb.I, T = pb.T, KB = H / kBlock, NCB = I / kBlock;
@@ -545,6 +555,8 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
     issue(j + kBgStages - 1);
   }
   MOEFP8_WAIT_VMCNT(0);
+  // the workgroup's next unit, claimed now so that the atomic overlaps the epilogue
+  if (threadIdx.x == 0) *next_s = grab_unit(pl.queues, n_units);
 
   // epilogue: C = silu(gate) * up, per-row max over the unit's 128 columns, hi/lo split
   const int col0 = cb * kBlock + 32 * wn;
@@ -606,7 +618,7 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Pl
   __shared__ int next_s;
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
   const int n_units = pl.info[2] * NCB;
-  if (threadIdx.x == 0) next_s = grab_unit(pl.queues, n_units);
+  if (threadIdx.x == 0) next_s = first_unit(pl.queues, n_units);
   __syncthreads();
   for (int v = uniform(next_s); v >= 0; v = uniform(next_s)) {
     const int2 uc = unit_at(pl.mbgroup1, v, NCB);
@@ -616,23 +628,23 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Pl
     // the previous unit's readers are done with the ring, amax_s and sw_s, and every thread has
     // read next_s
     __syncthreads();
-    // weight scales of the unit: {up, gate} per K-block; the next unit
+    // weight scales of the unit: {up, gate} per K-block
     {
       const float* su = pb.s13 + ((size_t)e * (2 * I / kBlock) + cb) * KB;
       const float* sg = su + (size_t)NCB * KB;
       const int t = threadIdx.x;
       if (t < KB) sw_s[t] = float2{su[t], sg[t]};
-      if (t == 0) next_s = grab_unit(pl.queues, n_units);
     }
     __syncthreads();
-    if (flags & kFlagExactProducts)
-      gemm1_big_unit<1, true>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
-    else if (rows <= 32)
-      gemm1_big_unit<1, false>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
-    else if (rows <= 64)
-      gemm1_big_unit<2, false>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
-    else
-      gemm1_big_unit<4, false>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags);
+#define MOEFP8_G1_UNIT(NT, EXACT) \
+  gemm1_big_unit<NT, EXACT>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags, &next_s, n_units)
+    if (flags & kFlagExactProducts) MOEFP8_G1_UNIT(1, true);
+    else if (rows <= 32) MOEFP8_G1_UNIT(1, false);
+    else if (rows <= 64) MOEFP8_G1_UNIT(2, false);
+    else MOEFP8_G1_UNIT(4, false);
+#undef MOEFP8_G1_UNIT
+    // next_s is written
+    __syncthreads();
   }
 }
 
@@ -818,8 +830,9 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
   constexpr int NP = MT / 2;
   __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
   const int H = pb.H, HB = H / kBlock;
-  const UnitWalk w = unit_walk(pl.info[5] * HB);
-  for (int v = w.v; v < w.end; v += w.step) {
+  const UnitEighths u;
+  const int n_units = pl.info[5] * HB, end = u.lo(n_units, u.x + 1);
+  for (int v = u.lo(n_units, u.x) + (int)blockIdx.x / u.nx; v < end; v += u.per) {
     const int2 uc = unit_at(pl.mbgroup2, v, HB);
     const int mb = uniform(uc.x), hb = uniform(uc.y);
     const int4 blk = pl.mblocks2[mb];
@@ -896,7 +909,8 @@ __device__ __forceinline__ void widen16(const v4i& x, float scale, v8h& t0, v8h&
 template <int kMode, int NT>
 __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float* sw2_s, int e, int row0, int rows,
-                                               int hc, float* __restrict__ obuf) {
+                                               int hc, float* __restrict__ obuf, int* queues, int* next_s,
+                                               int n_units) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
   static_assert(kMode != kPrecise || NT == 1, "exact-product blocks hold at most 32 rows");
   const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
@@ -1000,6 +1014,8 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
     issue(j + kB2Stages - 1);
   }
   MOEFP8_WAIT_VMCNT(0);
+  // the workgroup's next unit, claimed now so that the atomic overlaps the epilogue
+  if (threadIdx.x == 0) *next_s = grab_unit(queues, n_units);
 #pragma unroll
   for (int i = 0; i < NT; i++) {
     const int t = NT * wm + i;
@@ -1025,8 +1041,8 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
   __shared__ int next_s;
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
   const int n_units = pl.info[5] * HC;
-  int* queues = pl.queues + 8;
-  if (threadIdx.x == 0) next_s = grab_unit(queues, n_units);
+  int* queues = pl.queues + 8 * kQueueStride;
+  if (threadIdx.x == 0) next_s = first_unit(queues, n_units);
   __syncthreads();
   for (int v = uniform(next_s); v >= 0; v = uniform(next_s)) {
     const int2 uc = unit_at(pl.mbgroup2, v, HC);
@@ -1035,24 +1051,27 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
     // the previous unit's readers are done with the ring and sw2_s, and every thread has read next_s
     __syncthreads();
-    // W2 block scales of the unit's two 128-column blocks, per 128-K block; the next unit
+    // W2 block scales of the unit's two 128-column blocks, per 128-K block
     {
       const int t = threadIdx.x;
       if (t < 2 * KB) sw2_s[t] = pb.s2[((size_t)e * HB + 2 * hc + (t & 1)) * KB + (t >> 1)];
-      if (t == 0) next_s = grab_unit(queues, n_units);
     }
     __syncthreads();
-    if (flags & kFlagExactProducts)
-      gemm2_big_unit<kPrecise, 1>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+#define MOEFP8_G2_UNIT(MODE, NT) \
+  gemm2_big_unit<MODE, NT>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf, queues, &next_s, n_units)
+    if (flags & kFlagExactProducts) MOEFP8_G2_UNIT(kPrecise, 1);
     else if (flags & kFlagTwoTermC) {
-      if (rows <= 32) gemm2_big_unit<kTwoTerms, 1>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
-      else if (rows <= 64) gemm2_big_unit<kTwoTerms, 2>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
-      else gemm2_big_unit<kTwoTerms, 4>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+      if (rows <= 32) MOEFP8_G2_UNIT(kTwoTerms, 1);
+      else if (rows <= 64) MOEFP8_G2_UNIT(kTwoTerms, 2);
+      else MOEFP8_G2_UNIT(kTwoTerms, 4);
     } else {
-      if (rows <= 32) gemm2_big_unit<kOneTerm, 1>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
-      else if (rows <= 64) gemm2_big_unit<kOneTerm, 2>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
-      else gemm2_big_unit<kOneTerm, 4>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf);
+      if (rows <= 32) MOEFP8_G2_UNIT(kOneTerm, 1);
+      else if (rows <= 64) MOEFP8_G2_UNIT(kOneTerm, 2);
+      else MOEFP8_G2_UNIT(kOneTerm, 4);
     }
+#undef MOEFP8_G2_UNIT
+    // next_s is written
+    __syncthreads();
   }
 }
 

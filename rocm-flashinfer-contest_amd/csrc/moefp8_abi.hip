@@ -104,7 +104,7 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.mblocks2 = take((size_t)L.max_blocks2 * 16);
   L.mbgroup1 = take((size_t)L.max_blocks1 * 8);
   L.mbgroup2 = take((size_t)L.max_blocks2 * 8);
-  L.queues = take((size_t)kUnitQueues * 4);
+  L.queues = take((size_t)kUnitQueues * kQueueStride * 4);
   L.c_hi = take((size_t)pmax * I * 2);
   L.c_lo = take((size_t)pmax * I);
   L.c_lo16 = take((size_t)pmax * I * 2);

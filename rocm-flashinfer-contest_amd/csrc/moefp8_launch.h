@@ -67,7 +67,7 @@ struct Plan {
                               // blocks (one precision mode per block); info[5] blocks in all
   const int2* mbgroup1;       // large T: per m-block {first m-block of its expert, the expert's m-blocks}
   const int2* mbgroup2;
-  int* queues;                // large T: per-XCD unit queues of the 128-row GEMM1 (0..7) and GEMM2 (8..15)
+  int* queues;                // large T: per-XCD unit queues of GEMM1 (0..7) and GEMM2 (8..15), kQueueStride apart
   const int* canon_token;     // token of each pair in canonical (expert, token) order
   int* counters;              // small T: arrivals per (m-tile, 128 C columns), zeroed by the routing
   int* counters2;             // small T: arrivals per 64 output columns, zeroed by the routing
@@ -99,6 +99,7 @@ void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, flo
                         hipStream_t stream);
 
 constexpr int kUnitQueues = 16;
+constexpr int kQueueStride = 64;   // ints between queue counters: one 256-byte line each
 
 // Large-T path (T > 64).  Permutation arguments: pair counts per (block of 256 tokens,
 // bucket = local expert x magnitude class) and the outputs of the three launches.
@@ -124,7 +125,7 @@ struct LargePermArgs {
   int4* mblocks2;       // GEMM2 m-blocks
   int2* mbgroup1;       // per GEMM1 m-block: {first m-block of its expert, the expert's m-blocks}
   int2* mbgroup2;       // the same for GEMM2
-  int* queues;          // [kUnitQueues] unit queues of the 128-row GEMMs, zeroed here
+  int* queues;          // [kUnitQueues * kQueueStride] unit queues of the grouped GEMMs, zeroed here
   int rows_a;           // block height over an expert's class 0 and 1 rows
   int rows_b;           // block height over its class 2 (exact-product) rows
 };

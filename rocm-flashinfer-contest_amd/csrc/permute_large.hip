@@ -90,7 +90,7 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
   __shared__ int tot[kEGlobal * kClasses];
   __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], eb1[kEGlobal + 1], eb2[kEGlobal + 1];
   const int E = a.E_local, E3 = E * kClasses, nb = a.nblk, tid = threadIdx.x, lane = lane_id();
-  if (tid < kUnitQueues) a.queues[tid] = 0;
+  if (tid < kUnitQueues) a.queues[tid * kQueueStride] = 0;
 
   // canonical per-block base of each expert (relative), from the raw counts
   for (int e = tid; e < E; e += kScanThreads) {
