@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOEFP8_ABI_VERSION 3
+#define MOEFP8_ABI_VERSION 4
 
 /* Operator constants (solutions/moe_fp8/main.py:22-29). */
 #define MOEFP8_E_GLOBAL 256
@@ -97,6 +97,14 @@ typedef struct moefp8_args {
    * the last one after the combine, so stage i's device time is
    * hipEventElapsedTime(ev[i], ev[i+1]).  Used for live per-kernel timing. */
   void* stage_events;
+  /* optional, may be NULL: [T, H] dense rows in shared_dtype (MOEFP8_DTYPE_F32 or
+   * MOEFP8_DTYPE_BF16, 16-byte aligned) added to each token's routed sum in fp32 before its
+   * single bf16 rounding: output[t] = bf16(sum_e w_e O_e[t] + shared_output[t]).  This is
+   * DeepSeek-V3's shared-expert add fused into the combine (no counterpart in the reference
+   * operator, whose callers add the shared expert's output afterwards).  Tokens with no local
+   * expert get bf16(shared_output[t]). */
+  const void* shared_output;
+  int32_t shared_dtype;
 } moefp8_args;
 
 #define MOEFP8_NUM_STAGE_EVENTS 7

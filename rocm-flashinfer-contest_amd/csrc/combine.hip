@@ -1,7 +1,8 @@
 // Combine (main.py:241-243): each token's pair rows, summed in ascending expert order
 // starting from zero (the order of index_add_ in the reference), rounded once to bf16.
 // Tokens without a local expert get exact zero rows.  Pair rows may come split over K
-// (small-T GEMM2); the splits of a pair are added first, in ascending order.
+// (small-T GEMM2); the splits of a pair are added first, in ascending order.  An optional
+// shared row (the shared expert's output) is added last, before the rounding.
 #include "moefp8_device.h"
 #include "moefp8_launch.h"
 
@@ -13,7 +14,8 @@ constexpr int kCombineCols = 1024;
 __global__ __launch_bounds__(256) void combine_kernel(const int* __restrict__ tok_slot,
                                                       const int* __restrict__ info,
                                                       const float* __restrict__ obuf,
-                                                      uint16_t* __restrict__ out, int H) {
+                                                      uint16_t* __restrict__ out, int H, const void* shared,
+                                                      int shared_dt) {
   const int t = blockIdx.x;
   const int c = blockIdx.y * kCombineCols + 4 * threadIdx.x;
   const int S = info[4];
@@ -55,6 +57,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const int* __restrict__ to
       acc.w += o.w;
     }
   }
+  if (shared) add_shared4(acc, shared, shared_dt, (size_t)t * H + c);
   uint2 o;
   o.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
   o.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
@@ -65,7 +68,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const int* __restrict__ to
 void launch_combine(const Plan& pl, const float* obuf, uint16_t* out, int T, int H, hipStream_t stream) {
   if (T <= 0) return;
   hipLaunchKernelGGL(combine_kernel, dim3(T, (H + kCombineCols - 1) / kCombineCols), dim3(256), 0, stream,
-                     pl.tok_slot, pl.info, obuf, out, H);
+                     pl.tok_slot, pl.info, obuf, out, H, pl.shared, pl.shared_dt);
 }
 
 }  // namespace moefp8

@@ -385,7 +385,8 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
 // a row first, summed from zero in fp32 and rounded once to bf16; tokens without a local
 // expert get zeros.  Thread = (token, 4 columns).
 __device__ void combine_columns(const int* __restrict__ tok_slot, const float* __restrict__ obuf,
-                                uint16_t* __restrict__ out, int T, int H, int S, int c0) {
+                                uint16_t* __restrict__ out, int T, int H, int S, int c0, const void* shared,
+                                int shared_dt) {
   constexpr int kQuads = 16;                            // 4-column groups of the 64 columns
   const int c = c0 + 4 * (threadIdx.x % kQuads);
   for (int t = threadIdx.x / kQuads; t < T; t += blockDim.x / kQuads) {
@@ -441,6 +442,7 @@ __device__ void combine_columns(const int* __restrict__ tok_slot, const float* _
       acc.z += o.z;
       acc.w += o.w;
     }
+    if (shared) add_shared4(acc, shared, shared_dt, (size_t)t * H + c);
     uint2 v;
     v.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
     v.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
@@ -466,10 +468,16 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
   const int n_units = n_mt * S * NCB;
   const int wave = wave_index();
   if (n_units == 0) {
-    // no local pairs: every output row is zero
+    // no local pairs: every output row is zero (plus the shared row)
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < (size_t)T * H / 4;
-         i += (size_t)gridDim.x * blockDim.x)
-      reinterpret_cast<uint2*>(out)[i] = uint2{0u, 0u};
+         i += (size_t)gridDim.x * blockDim.x) {
+      float4 acc = {0.f, 0.f, 0.f, 0.f};
+      if (pl.shared) add_shared4(acc, pl.shared, pl.shared_dt, 4 * i);
+      uint2 v;
+      v.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
+      v.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
+      reinterpret_cast<uint2*>(out)[i] = v;
+    }
     return;
   }
 
@@ -651,7 +659,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     // output columns [64 cb, 64 cb + 64) are complete once all n_mt * S units of the column
     // block stored their rows
     if (arrive_last(pl.counters2 + du.cb, n_mt * S, &last_s))
-      combine_columns(pl.tok_slot, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves);
+      combine_columns(pl.tok_slot, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves, pl.shared, pl.shared_dt);
   }
 }
 

@@ -231,6 +231,24 @@ __device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
   return dt == 1 ? bf16_to_f32(h) : half_to_f32(h);
 }
 
+// acc += the 4 consecutive elements [i, i + 4) of a shared row of dtype dt (0 f32, 1 bf16),
+// the last term of a token's combine.
+__device__ __forceinline__ void add_shared4(float4& acc, const void* shared, int dt, size_t i) {
+  if (dt == 0) {
+    const float4 v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(shared) + i);
+    acc.x += v.x;
+    acc.y += v.y;
+    acc.z += v.z;
+    acc.w += v.w;
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(shared) + i);
+    acc.x += __uint_as_float(v.x << 16);
+    acc.y += __uint_as_float(v.x & 0xffff0000u);
+    acc.z += __uint_as_float(v.y << 16);
+    acc.w += __uint_as_float(v.y & 0xffff0000u);
+  }
+}
+
 __device__ __forceinline__ float silu_f32(float x) {
   return __fdiv_rn(x, 1.0f + __expf(-x));
 }

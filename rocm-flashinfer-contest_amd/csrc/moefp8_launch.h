@@ -71,6 +71,8 @@ struct Plan {
   const int* canon_token;     // token of each pair in canonical (expert, token) order
   int* counters;              // small T: arrivals per (m-tile, 128 C columns), zeroed by the routing
   int* counters2;             // small T: arrivals per 64 output columns, zeroed by the routing
+  const void* shared;         // optional [T, H] rows added before the bf16 rounding (NULL: none)
+  int shared_dt;              // 0 fp32, 1 bf16
 };
 
 struct Problem {

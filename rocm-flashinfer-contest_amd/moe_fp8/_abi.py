@@ -12,7 +12,7 @@ from pathlib import Path
 LIB_NAME = "libmoefp8.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -59,6 +59,8 @@ class MoeFp8Args(ctypes.Structure):
         ("expert_offsets", ctypes.c_void_p),
         ("permuted_tokens", ctypes.c_void_p),
         ("stage_events", ctypes.c_void_p),
+        ("shared_output", ctypes.c_void_p),
+        ("shared_dtype", ctypes.c_int32),
     ]
 
 

@@ -90,7 +90,7 @@ def _scalar(x, kind):
 
 def _prepare(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
              gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
-             routed_scaling_factor, debug=None):
+             routed_scaling_factor, debug=None, shared_output=None):
     """Check the arguments, allocate output + workspace, fill the C argument struct."""
     lib = _abi.load()
     if not isinstance(hidden_states, torch.Tensor) or hidden_states.device.type != "cuda":
@@ -148,14 +148,30 @@ def _prepare(routing_logits, routing_bias, hidden_states, hidden_states_scale, g
         args.topk_weights = debug["topk_weights"].data_ptr()
         args.expert_offsets = debug["expert_offsets"].data_ptr()
         args.permuted_tokens = debug["permuted_tokens"].data_ptr()
-    keep = (logits, bias, hs, hss, w13, s13, w2, s2)      # keep contiguous copies alive
+    shared = None
+    if shared_output is not None:
+        if not isinstance(shared_output, torch.Tensor) or shared_output.device != device:
+            raise ValueError(f"shared_output must be a tensor on {device}")
+        if tuple(shared_output.shape) != (T, Hd):
+            raise ValueError(f"shared_output: shape {tuple(shared_output.shape)} != ({T}, {Hd})")
+        if shared_output.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError(f"shared_output: expected float32 or bfloat16, got {shared_output.dtype}")
+        shared = shared_output.contiguous()
+        args.shared_output = shared.data_ptr()
+        args.shared_dtype = _DT[shared.dtype]
+    keep = (logits, bias, hs, hss, w13, s13, w2, s2, shared)      # keep contiguous copies alive
     return lib, args, out, ws, ws_bytes, keep
 
 
 def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
         gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
-        routed_scaling_factor, *, debug=None):
+        routed_scaling_factor, *, shared_output=None, debug=None):
     """Same contract as ``solutions/moe_fp8/main.py:173-243``.
+
+    ``shared_output`` (optional, keyword only; no counterpart in the reference): a [T, H]
+    float32 or bfloat16 device tensor, e.g. DeepSeek-V3's shared-expert output, added to each
+    token's routed sum in fp32 before the single bf16 rounding (the add fused into the
+    combine instead of a separate pass over the output).
 
     ``debug`` (optional dict) receives the device tensors ``topk_ids`` [T, 8]
     int32 (ascending global ids), ``topk_weights`` [T, 8] fp32,
@@ -164,7 +180,7 @@ def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_
     """
     lib, args, out, ws, ws_bytes, _keep = _prepare(
         routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
-        gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor, debug)
+        gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor, debug, shared_output)
     if args.num_tokens == 0:
         return out
     device = out.device
@@ -179,9 +195,9 @@ class Runner:
     construction and every call only crosses the C ABI (for timing loops and
     serving loops that reuse the same buffers).  Each call overwrites ``out``."""
 
-    def __init__(self, *run_args, debug=None):
+    def __init__(self, *run_args, debug=None, shared_output=None):
         (self.lib, self.args, self.out, self.workspace, self.ws_bytes,
-         self._keep) = _prepare(*run_args, debug=debug)
+         self._keep) = _prepare(*run_args, debug=debug, shared_output=shared_output)
         self.device = self.out.device
 
     def __call__(self, stage_events=None, stream=None):

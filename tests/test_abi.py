@@ -42,6 +42,14 @@ def test_library_is_built_for_gfx950_only():
         assert other not in data
 
 
+def test_ctypes_struct_mirrors_the_header():
+    """Field names and order of struct moefp8_args in the header == the ctypes mirror."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = re.search(r"typedef struct moefp8_args \{(.*?)\} moefp8_args;", text, flags=re.S).group(1)
+    names = re.findall(r"(\w+)\s*;", body)
+    assert names == [f for f, _ in _abi.MoeFp8Args._fields_]
+
+
 def test_abi_version_and_strerror(lib):
     assert lib.moefp8_abi_version() == _abi.ABI_VERSION
     for code in _abi.STATUS:
@@ -94,6 +102,8 @@ def test_run_rejects_bad_arguments_before_any_launch(lib):
     assert run(_args(hidden_states=0x100001)) == -4
     assert run(_args(routing_logits=0x100002)) == -4              # fp32 logits need 16-byte rows
     assert run(_args(gemm1_weights_scale=0x100002)) == -4
+    assert run(_args(shared_output=0x100000 * 12, shared_dtype=2)) == -3   # shared rows: fp32 or bf16
+    assert run(_args(shared_output=0x100008, shared_dtype=1)) == -4
     assert run(_args(), n=1024) == -5                              # workspace too small
     assert run(_args(), w=0) == -5
     assert run(_args(num_tokens=0)) == 0                           # nothing to do, nothing launched

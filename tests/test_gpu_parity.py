@@ -168,6 +168,51 @@ def test_full_path_high_magnitude_tokens(T, E_local, H, I):
     assert_close(out, ref32, f"magnitude T={T}")
 
 
+@pytest.mark.parametrize("T,E_local,H,I,offset,sdt", [(16, 8, 512, 256, 0, torch.bfloat16),
+                                                      (16, 8, 512, 256, 0, torch.float32),
+                                                      (16, 8, 256, 128, 300, torch.float32),
+                                                      (300, 16, 512, 256, 0, torch.float32),
+                                                      (2100, 16, 512, 256, 0, torch.bfloat16)])
+def test_shared_output_fused_add(T, E_local, H, I, offset, sdt):
+    """The shared-expert rows are added in fp32 before the single bf16 rounding: the result
+    meets the bar against oracle + shared, equals the plain output for an all-zero shared
+    tensor, and is exactly bf16(shared) for tokens without a local expert (offset 300: no
+    local expert at all, the small-T path's zero-work branch)."""
+    print(f"[shared] T={T} E_local={E_local} H={H} I={I} offset={offset} {sdt}", flush=True)
+    wl = W.Workload(f"s{T}", T, 3000 + T)
+    weights = W.make_weights(E_local, H, I, device="cpu", seed=11 + E_local)
+    args = boosted(W.make_inputs(wl, device="cpu", E_local=E_local, H=H, I=I, weights=weights,
+                                 local_expert_offset=offset), E_local, offset)
+    g = torch.Generator().manual_seed(T)
+    shared = (torch.randn(T, H, generator=g) * 3.0).to(sdt)
+    dargs = to_dev(args)
+    plain = moe_fp8.run(*dargs)
+    fused = moe_fp8.run(*dargs, shared_output=shared.to(DEV))
+    zero = moe_fp8.run(*dargs, shared_output=torch.zeros(T, H, dtype=sdt, device=DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(zero.view(torch.int16), plain.view(torch.int16))
+    ref32, _ = O.moe_forward(*args)
+    assert_close(fused, ref32 + shared.float(), f"shared T={T} off={offset}")
+    ridx, _, _, _ = oracle_route(args[0], args[1])
+    nolocal = torch.from_numpy(~np.any((ridx >= offset) & (ridx < offset + E_local), axis=1))
+    if offset == 300:
+        assert bool(nolocal.all())
+    want = shared.float().to(torch.bfloat16)[nolocal]
+    assert torch.equal(fused.cpu()[nolocal].view(torch.int16), want.view(torch.int16))
+
+
+def test_shared_output_rejects_bad_tensors():
+    T, E_local, H, I = 4, 4, 256, 128
+    weights = W.make_weights(E_local, H, I, device="cpu", seed=2)
+    args = to_dev(W.make_inputs(W.Workload("b", T, 1), device="cpu", E_local=E_local, H=H, I=I, weights=weights))
+    with pytest.raises(ValueError):
+        moe_fp8.run(*args, shared_output=torch.zeros(T, H + 128, device=DEV))
+    with pytest.raises(TypeError):
+        moe_fp8.run(*args, shared_output=torch.zeros(T, H, dtype=torch.float16, device=DEV))
+    with pytest.raises(ValueError):
+        moe_fp8.run(*args, shared_output=torch.zeros(T, H))
+
+
 def test_golden_fixtures_full_path():
     from pathlib import Path
     for f in sorted((Path(__file__).resolve().parent / "golden").glob("moe_*.npz")):
