@@ -396,9 +396,9 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, 
   const UnitEighths u;
   const int n_units = pl.info[2] * NCB, end = u.lo(n_units, u.x + 1);
   for (int v = u.lo(n_units, u.x) + (int)blockIdx.x / u.nx; v < end; v += u.per) {
-    const int2 uc = unit_at(pl.mbgroup1, v, NCB);
+    const int2 uc = unit_at(pl.mbgroup, v, NCB);
     const int mb = uniform(uc.x), cb = uniform(uc.y);
-    const int4 blk = pl.mblocks1[mb];
+    const int4 blk = pl.mblocks[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
     const int mvalid = (rows + 15) / 16;
     if (!(flags & kFlagExactProducts)) {
@@ -600,7 +600,7 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
         const _Float16 hi = (_Float16)v;
         ch.hi[p * I + col] = hi;
         if constexpr (kExact) ch.lo16[p * I + col] = (_Float16)(v - (float)hi);
-        else if (two)   // GEMM2's two-term blocks (class 1 rows) read it
+        else if (two)   // GEMM2 reads it in blocks holding class 1 rows
           ch.lo[p * I + col] = (uint8_t)f32_to_e4m3(fminf(fmaxf((v - (float)hi) * kLoScale, -448.0f), 448.0f));
       }
       if (wn == 0 && lr == 0) ch.scale[p * NCB + cb] = scale;
@@ -621,9 +621,9 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Pl
   if (threadIdx.x == 0) next_s = first_unit(pl.queues, n_units);
   __syncthreads();
   for (int v = uniform(next_s); v >= 0; v = uniform(next_s)) {
-    const int2 uc = unit_at(pl.mbgroup1, v, NCB);
+    const int2 uc = unit_at(pl.mbgroup, v, NCB);
     const int mb = uniform(uc.x), cb = uniform(uc.y);
-    const int4 blk = pl.mblocks1[mb];
+    const int4 blk = pl.mblocks[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
     // the previous unit's readers are done with the ring, amax_s and sw_s, and every thread has
     // read next_s
@@ -831,11 +831,11 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
   __shared__ __attribute__((aligned(16))) uint8_t ring[kLgStages * L::kStage];
   const int H = pb.H, HB = H / kBlock;
   const UnitEighths u;
-  const int n_units = pl.info[5] * HB, end = u.lo(n_units, u.x + 1);
+  const int n_units = pl.info[2] * HB, end = u.lo(n_units, u.x + 1);
   for (int v = u.lo(n_units, u.x) + (int)blockIdx.x / u.nx; v < end; v += u.per) {
-    const int2 uc = unit_at(pl.mbgroup2, v, HB);
+    const int2 uc = unit_at(pl.mbgroup, v, HB);
     const int mb = uniform(uc.x), hb = uniform(uc.y);
-    const int4 blk = pl.mblocks2[mb];
+    const int4 blk = pl.mblocks[mb];
     const int e = uniform(blk.x), flags = uniform(blk.w);
     for (int s0 = 0; s0 < blk.z; s0 += 16 * MT) {
       const int row0 = uniform(blk.y + s0), rows = uniform(min(16 * MT, blk.z - s0));
@@ -862,7 +862,7 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
 }
 
 // ------------------------------------------------------------------------------ GEMM2, 128-row m-blocks
-// For the 128-row class 0 (one term of C) and class 1 (two terms) blocks.  A workgroup of 8
+// For the 128-row blocks (one term of C, or two in blocks holding class 1 rows).  A workgroup of 8
 // wavefronts (one per CU, two per SIMD) owns one unit = (m-block, 256 output columns) and stages
 // C's hi term (f16), its lo term (e4m3, two-term blocks) and the W2 rows by DMA through a 3-stage
 // LDS ring, 64 K per stage.  Wavefront (wm, wn) = (w % 2, w / 2) computes rows 64 wm .. +63 x
@@ -1040,14 +1040,14 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
   const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock, HC = H / kB2Cols;
   __shared__ int next_s;
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
-  const int n_units = pl.info[5] * HC;
+  const int n_units = pl.info[2] * HC;
   int* queues = pl.queues + 8 * kQueueStride;
   if (threadIdx.x == 0) next_s = first_unit(queues, n_units);
   __syncthreads();
   for (int v = uniform(next_s); v >= 0; v = uniform(next_s)) {
-    const int2 uc = unit_at(pl.mbgroup2, v, HC);
+    const int2 uc = unit_at(pl.mbgroup, v, HC);
     const int mb = uniform(uc.x), hc = uniform(uc.y);
-    const int4 blk = pl.mblocks2[mb];
+    const int4 blk = pl.mblocks[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
     // the previous unit's readers are done with the ring and sw2_s, and every thread has read next_s
     __syncthreads();

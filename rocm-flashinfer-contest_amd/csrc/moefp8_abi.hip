@@ -37,9 +37,9 @@ int large_rows_b(int64_t T, int H, int I) { return large_big(T, H, I) ? kExactRo
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
   size_t tok_a2, esig, mtiles, counters, c16, c16_scale, gbuf, obuf;
-  size_t canon_token, bcnt, ccnt, mblocks1, mblocks2, mbgroup1, mbgroup2, queues, c_hi, c_lo, c_lo16, c_scale;
+  size_t canon_token, bcnt, ccnt, mblocks, mbgroup, queues, c_hi, c_lo, c_lo16, c_scale;
   size_t total;
-  int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks1, max_blocks2, n_counters1, n_counters;
+  int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks, n_counters1, n_counters;
   int nblk;
 };
 
@@ -92,18 +92,14 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.rows_cap = pmax;
   L.nblk = permute_large_blocks(T);
   const int ra = large_rows_a(T, H, I), rb = large_rows_b(T, H, I);
-  // blocks per expert: GEMM1 ceil(class 0+1 rows / ra) + ceil(class 2 rows / rb); GEMM2 has the
-  // class 0 and class 1 rows in separate blocks (one more partial block per expert)
+  // blocks per expert (both GEMMs): ceil(class 0+1 rows / ra) + ceil(class 2 rows / rb)
   const int64_t exact_blocks = (pmax + rb - 1) / rb + E_local;
-  L.max_blocks1 = (pmax + ra - 1) / ra + E_local + exact_blocks;
-  L.max_blocks2 = (pmax + ra - 1) / ra + 2 * E_local + exact_blocks;
+  L.max_blocks = (pmax + ra - 1) / ra + E_local + exact_blocks;
   L.canon_token = take((size_t)pmax * 4);
   L.bcnt = take((size_t)L.nblk * E_local * 3 * 4);
   L.ccnt = take((size_t)L.nblk * E_local * 4);
-  L.mblocks1 = take((size_t)L.max_blocks1 * 16);
-  L.mblocks2 = take((size_t)L.max_blocks2 * 16);
-  L.mbgroup1 = take((size_t)L.max_blocks1 * 8);
-  L.mbgroup2 = take((size_t)L.max_blocks2 * 8);
+  L.mblocks = take((size_t)L.max_blocks * 16);
+  L.mbgroup = take((size_t)L.max_blocks * 8);
   L.queues = take((size_t)kUnitQueues * kQueueStride * 4);
   L.c_hi = take((size_t)pmax * I * 2);
   L.c_lo = take((size_t)pmax * I);
@@ -279,10 +275,8 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pl.mtile_offsets = reinterpret_cast<int*>(ws + L.mtile_offsets);
   pl.info = reinterpret_cast<int*>(ws + L.info);
   pl.mtiles = nullptr;
-  pl.mblocks1 = nullptr;
-  pl.mblocks2 = nullptr;
-  pl.mbgroup1 = nullptr;
-  pl.mbgroup2 = nullptr;
+  pl.mblocks = nullptr;
+  pl.mbgroup = nullptr;
   pl.queues = nullptr;
   pl.canon_token = pl.perm_token;
   pl.counters = nullptr;
@@ -376,18 +370,14 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pa.perm_w = const_cast<float*>(pl.perm_w);
   pa.canon_token = reinterpret_cast<int*>(ws + L.canon_token);
   pa.tok_slot = const_cast<int*>(pl.tok_slot);
-  pa.mblocks1 = reinterpret_cast<int4*>(ws + L.mblocks1);
-  pa.mblocks2 = reinterpret_cast<int4*>(ws + L.mblocks2);
-  pa.mbgroup1 = reinterpret_cast<int2*>(ws + L.mbgroup1);
-  pa.mbgroup2 = reinterpret_cast<int2*>(ws + L.mbgroup2);
+  pa.mblocks = reinterpret_cast<int4*>(ws + L.mblocks);
+  pa.mbgroup = reinterpret_cast<int2*>(ws + L.mbgroup);
   pa.queues = reinterpret_cast<int*>(ws + L.queues);
   pa.rows_a = large_rows_a(T, H, I);
   pa.rows_b = large_rows_b(T, H, I);
   pl.canon_token = pa.canon_token;
-  pl.mblocks1 = pa.mblocks1;
-  pl.mblocks2 = pa.mblocks2;
-  pl.mbgroup1 = pa.mbgroup1;
-  pl.mbgroup2 = pa.mbgroup2;
+  pl.mblocks = pa.mblocks;
+  pl.mbgroup = pa.mbgroup;
   pl.queues = pa.queues;
   CHalf8 ch;
   ch.hi = reinterpret_cast<_Float16*>(ws + L.c_hi);
@@ -402,16 +392,16 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   launch_permute_large(pa, s);
   mark(2);
   if (large_big(T, H, I)) {
-    launch_gemm1_big(pb, pl, ch, (int)(L.max_blocks1 * (I / kBlock)), s);
+    launch_gemm1_big(pb, pl, ch, (int)(L.max_blocks * (I / kBlock)), s);
   } else {
-    launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks1 * (I / kBlock)), s);
+    launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks * (I / kBlock)), s);
   }
   mark(3);
   mark(4);   // SwiGLU is GEMM1's epilogue here: empty activation stage
   if (large_big(T, H, I)) {
-    launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks2 * (H / 256)), s);
+    launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks * (H / 256)), s);
   } else {
-    launch_gemm2_large(pb, pl, ch, obuf, large_mt(T), (int)(L.max_blocks2 * (H / kBlock)), s);
+    launch_gemm2_large(pb, pl, ch, obuf, large_mt(T), (int)(L.max_blocks * (H / kBlock)), s);
   }
   mark(5);
   launch_combine(pl, obuf, a->output, (int)T, H, s);

@@ -60,13 +60,11 @@ struct Plan {
   const int* mtile_offsets;   // [E_local + 1]
   const int* info;            // {P, n_active, GEMM1 m-blocks|m-tiles, S1, S2, GEMM2 m-blocks, m-tiles}
   const int4* mtiles;         // small T: per m-tile {expert, first pair, rows, OR of pair flags}
-  const int4* mblocks1;       // large T, GEMM1: m-blocks {expert, first row, rows, flags}, expert by
-                              // expert: its class 0 and 1 rows together, then its exact-product rows;
-                              // info[2] blocks in all
-  const int4* mblocks2;       // large T, GEMM2: the same with class 0 and class 1 rows in separate
-                              // blocks (one precision mode per block); info[5] blocks in all
-  const int2* mbgroup1;       // large T: per m-block {first m-block of its expert, the expert's m-blocks}
-  const int2* mbgroup2;
+  const int4* mblocks;        // large T, both GEMMs: m-blocks {expert, first row, rows, flags}, expert by
+                              // expert: its class 0 and 1 rows together (two-term C where a block
+                              // holds class 1 rows), then its exact-product rows; info[2] (= info[5])
+                              // blocks in all
+  const int2* mbgroup;        // large T: per m-block {first m-block of its expert, the expert's m-blocks}
   int* queues;                // large T: per-XCD unit queues of GEMM1 (0..7) and GEMM2 (8..15), kQueueStride apart
   const int* canon_token;     // token of each pair in canonical (expert, token) order
   int* counters;              // small T: arrivals per (m-tile, 128 C columns), zeroed by the routing
@@ -123,10 +121,8 @@ struct LargePermArgs {
   float* perm_w;        // [Pmax]
   int* canon_token;     // [Pmax] canonical order
   int* tok_slot;        // [T * 8] internal rows of each token's pairs, ascending expert
-  int4* mblocks1;       // GEMM1 m-blocks {expert, first row, rows, flags}
-  int4* mblocks2;       // GEMM2 m-blocks
-  int2* mbgroup1;       // per GEMM1 m-block: {first m-block of its expert, the expert's m-blocks}
-  int2* mbgroup2;       // the same for GEMM2
+  int4* mblocks;        // m-blocks of both GEMMs {expert, first row, rows, flags}
+  int2* mbgroup;        // per m-block: {first m-block of its expert, the expert's m-blocks}
   int* queues;          // [kUnitQueues * kQueueStride] unit queues of the grouped GEMMs, zeroed here
   int rows_a;           // block height over an expert's class 0 and 1 rows
   int rows_b;           // block height over its class 2 (exact-product) rows
@@ -150,7 +146,7 @@ void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int
 constexpr int kBigRows = 128;
 constexpr int kBigMaxKB = 64;   // H <= 8192
 void launch_gemm1_big(const Problem& pb, const Plan& pl, const CHalf8& ch, int max_units, hipStream_t stream);
-// GEMM2 over its blocks [0, info[5]), blocks taken 16 * mt rows at a time
+// GEMM2 over the blocks [0, info[2]), taken 16 * mt rows at a time
 void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
                         hipStream_t stream);
 // GEMM2 over the whole table, 256 output columns per unit

@@ -88,7 +88,7 @@ __device__ __forceinline__ int wave_exclusive_sum(int v) {
 
 __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a) {
   __shared__ int tot[kEGlobal * kClasses];
-  __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], eb1[kEGlobal + 1], eb2[kEGlobal + 1];
+  __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], eb1[kEGlobal + 1];
   const int E = a.E_local, E3 = E * kClasses, nb = a.nblk, tid = threadIdx.x, lane = lane_id();
   if (tid < kUnitQueues) a.queues[tid * kQueueStride] = 0;
 
@@ -114,13 +114,14 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
     tot[i] = run;
   }
   __syncthreads();
-  // expert offsets, 16-row m-tile offsets and m-block offsets, expert by expert.  GEMM1: blocks of
-  // rows_a rows over an expert's class 0 and 1 rows; GEMM2: blocks of rows_a rows over its class 0
-  // rows, then over its class 1 rows (one precision mode per block); both: then blocks of rows_b
-  // rows over its class 2 rows.  An expert's blocks are consecutive, so the units that stream its
+  // expert offsets, 16-row m-tile offsets and m-block offsets, expert by expert: blocks of rows_a
+  // rows over an expert's class 0 and 1 rows (two-term C in the blocks that hold class 1 rows),
+  // then blocks of rows_b rows over its class 2 rows; both GEMMs run this one table (GEMM2 on
+  // separate class 0 and class 1 blocks had 11% more blocks, hence more weight streams, and was
+  // 4% slower at T = 8192).  An expert's blocks are consecutive, so the units that stream its
   // weights run close together in time and share them through L2.
   if (tid < kWave) {
-    int carry = 0, carry_mt = 0, carry_1 = 0, carry_2 = 0, carry_act = 0;
+    int carry = 0, carry_mt = 0, carry_1 = 0, carry_act = 0;
     for (int e0 = 0; e0 < E; e0 += kWave) {
       const int e = e0 + lane;
       const int n0 = e < E ? tot[kClasses * e] : 0, n1 = e < E ? tot[kClasses * e + 1] : 0;
@@ -128,15 +129,13 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
       const int mt = (n + 15) / 16;
       const int bx = (n2 + a.rows_b - 1) / a.rows_b;
       const int b1 = (n0 + n1 + a.rows_a - 1) / a.rows_a + bx;
-      const int b2 = (n0 + a.rows_a - 1) / a.rows_a + (n1 + a.rows_a - 1) / a.rows_a + bx;
       const int pn = wave_exclusive_sum(n), pmt = wave_exclusive_sum(mt);
-      const int p1 = wave_exclusive_sum(b1), p2 = wave_exclusive_sum(b2);
+      const int p1 = wave_exclusive_sum(b1);
       const uint64_t act = __ballot(n > 0);
       if (e < E) {
         eoff[e] = carry + pn;
         emt[e] = carry_mt + pmt;
         eb1[e] = carry_1 + p1;
-        eb2[e] = carry_2 + p2;
         a.expert_offsets[e] = carry + pn;
         a.mtile_offsets[e] = carry_mt + pmt;
         if (n > 0) a.active[carry_act + lanes_below(act)] = e;
@@ -144,14 +143,12 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
       carry += __builtin_amdgcn_readlane(pn + n, kWave - 1);
       carry_mt += __builtin_amdgcn_readlane(pmt + mt, kWave - 1);
       carry_1 += __builtin_amdgcn_readlane(p1 + b1, kWave - 1);
-      carry_2 += __builtin_amdgcn_readlane(p2 + b2, kWave - 1);
       carry_act += (int)__popcll(act);
     }
     if (lane == 0) {
       eoff[E] = carry;
       emt[E] = carry_mt;
       eb1[E] = carry_1;
-      eb2[E] = carry_2;
       a.expert_offsets[E] = carry;
       a.mtile_offsets[E] = carry_mt;
       a.info[0] = carry;                // P
@@ -159,7 +156,7 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
       a.info[2] = carry_1;              // GEMM1 m-blocks
       a.info[3] = 1;                    // K-splits (small-T GEMMs only)
       a.info[4] = 1;
-      a.info[5] = carry_2;              // GEMM2 m-blocks
+      a.info[5] = carry_1;              // GEMM2 m-blocks: the same table
       a.info[6] = carry_mt;             // 16-row m-tiles
     }
   }
@@ -178,28 +175,12 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
     const int ba = (c01 + a.rows_a - 1) / a.rows_a;
     if (j < ba) {
       const int r0 = j * a.rows_a, rows = min(a.rows_a, c01 - r0);
-      a.mblocks1[g] = int4{e, eoff[e] + r0, rows, r0 + rows > c0 ? (int)class_flags(1) : 0};
+      a.mblocks[g] = int4{e, eoff[e] + r0, rows, r0 + rows > c0 ? (int)class_flags(1) : 0};
     } else {
       const int r0 = c01 + (j - ba) * a.rows_b;
-      a.mblocks1[g] = int4{e, eoff[e] + r0, min(a.rows_b, n - r0), (int)class_flags(2)};
+      a.mblocks[g] = int4{e, eoff[e] + r0, min(a.rows_b, n - r0), (int)class_flags(2)};
     }
-    a.mbgroup1[g] = int2{eb1[e], eb1[e + 1] - eb1[e]};
-  }
-  for (int g = tid; g < eb2[E]; g += kScanThreads) {
-    const int e = upper_bound(eb2, E + 1, g) - 1, j = g - eb2[e];
-    const int n0 = tot[kClasses * e], c01 = n0 + tot[kClasses * e + 1], n = eoff[e + 1] - eoff[e];
-    const int b0 = (n0 + a.rows_a - 1) / a.rows_a, b01 = b0 + (c01 - n0 + a.rows_a - 1) / a.rows_a;
-    if (j < b0) {
-      const int r0 = j * a.rows_a;
-      a.mblocks2[g] = int4{e, eoff[e] + r0, min(a.rows_a, n0 - r0), 0};
-    } else if (j < b01) {
-      const int r0 = n0 + (j - b0) * a.rows_a;
-      a.mblocks2[g] = int4{e, eoff[e] + r0, min(a.rows_a, c01 - r0), (int)class_flags(1)};
-    } else {
-      const int r0 = c01 + (j - b01) * a.rows_b;
-      a.mblocks2[g] = int4{e, eoff[e] + r0, min(a.rows_b, n - r0), (int)class_flags(2)};
-    }
-    a.mbgroup2[g] = int2{eb2[e], eb2[e + 1] - eb2[e]};
+    a.mbgroup[g] = int2{eb1[e], eb1[e + 1] - eb1[e]};
   }
 }
 
