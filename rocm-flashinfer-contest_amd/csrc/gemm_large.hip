@@ -449,6 +449,42 @@ constexpr int kBgOps = 2 + 4 + 1;            // per wavefront and K-block: A, B 
 
 __device__ __forceinline__ int bg_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
+// LDS row R of a 128-row unit -> row of the permuted pairs.  Regular blocks: R < rows.  A mixed
+// block (an expert's last regular block with its <= 32 exact-product rows folded in) puts its
+// regular rows at LDS rows [0, cap) and its exact rows at [cap, 128), cap = 128 - 16 ceil(x / 16);
+// the exact rows follow the regular ones in the permuted order.  Rows from xfrom on (0 for an
+// exact-product block, cap for a mixed one, 128 otherwise) get exact products and an f16 lo term.
+struct RowMap {
+  int row0, rows, cap, xrows, xfrom;
+  __device__ __forceinline__ int src(int R) const {
+    return R < cap ? row0 + min(R, rows - 1) : row0 + rows + min(R - cap, xrows - 1);
+  }
+  __device__ __forceinline__ bool valid(int R) const { return R < cap ? R < rows : R - cap < xrows; }
+};
+__device__ __forceinline__ RowMap row_map(int row0, int rows, int flags) {
+  if (flags & kFlagMixed) {
+    const int x = flags >> kMixedShift, cap = kBgRows - 16 * ((x + 15) / 16);
+    return RowMap{row0, rows, cap, x, cap};
+  }
+  return RowMap{row0, rows, kBgRows, 0, (flags & kFlagExactProducts) ? 0 : kBgRows};
+}
+
+// A mixed block's m-tiles for wavefront half wm: nf regular tiles from tf0 and nx exact tiles from
+// tx0.  An exact tile costs about three regular ones, so with two exact tiles each half takes one
+// of them and half of the regular tiles, and with one the other half takes more regular tiles.
+struct TileSplit {
+  int nf, nx, tf0, tx0;
+};
+__device__ __forceinline__ TileSplit mixed_split(const RowMap& rm, int wm) {
+  const int nr = (rm.rows + 15) / 16;
+  if (rm.cap == kBgRows - 32) {
+    const int a = (nr + 1) / 2;
+    return wm == 0 ? TileSplit{a, 1, 0, 6} : TileSplit{nr - a, 1, a, 7};
+  }
+  const int a = min(min(nr, 4), (nr + 4) / 2);
+  return wm == 0 ? TileSplit{a, 0, 0, 0} : TileSplit{nr - a, 1, a, 7};
+}
+
 // One unit.  Wavefront (wm, wn) computes m-tiles NT wm .. NT wm + NT - 1: NT = 4 for blocks of more
 // than 64 rows, 2 for 33..64 rows and 1 for at most 32 (the short last blocks of an expert's
 // classes cost a quarter of the MFMA and VALU work of a full one).  kExact (blocks of at most 32
@@ -608,8 +644,169 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
   }
 }
 
-// Units (m-block, 128 C columns) over GEMM1's blocks (128-row class 0/1 blocks and 32-row
-// exact-product blocks).
+// One unit of a mixed block.  This wavefront computes NF m-tiles tf0 .. tf0 + NF - 1 on the e4m3
+// MFMA and NX m-tiles tx0 .. tx0 + NX - 1 with exact products (the f16 MFMA on operands widened
+// exactly), its half of the block's tiles (mixed_split); every wavefront issues the same DMAs and
+// barriers.  (Kept apart from gemm1_big_unit: the compiler schedules the regular blocks' K loop
+// worse in this general form, LDS reads no longer hoisted ahead of the MFMAs, ~10% slower.)
+template <int NF, int NX>
+__device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
+                                               uint32_t ring_lds, const float2* sw_s, float (*amax_s)[kBgRows],
+                                               int e, const RowMap& rm, int cb, bool two, int tf0, int tx0,
+                                               int* next_s, int n_units) {
+  constexpr int NT = NF + NX;
+  static_assert(NT >= 1 && NT <= 4, "m-tiles per wavefront");
+  const int H = pb.H, I = pb.I, T = pb.T, KB = H / kBlock, NCB = I / kBlock;
+  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  const int wn = wave >> 1;
+  auto tile = [&](int i) { return i < NF ? tf0 + i : tx0 + (i - NF); };
+  // DMA lane roles: row (lane / 8) of an 8-row group, slot lane % 8
+  const int drow = lane >> 3, dslot = lane & 7;
+  // operand read offsets inside a 16-row tile (swizzled chunks 2kg and 2kg + 1 of row lr)
+  const int rd0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
+  const int rd1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
+  // DMA sources as per-lane byte offsets from wave-uniform bases: A rows 16w + 8q + drow (the
+  // tokens' hidden rows), B LDS rows 32w + 8q + drow (LDS row R holds n-tile (R % 64) / 16 of
+  // weight-row group R / 64: 0, 1 up, 2, 3 gate), row scales of rows 64 (w % 2) + lane
+  uint32_t aoff[2], boff[4];
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int r = 16 * wave + 8 * q + drow;
+    const int tok = pl.perm_token[rm.src(r)];
+    aoff[q] = (uint32_t)tok * (uint32_t)H + (uint32_t)((dslot ^ bg_key(r)) * 16);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int R = 32 * wave + 8 * q + drow;
+    const int g = R >> 6, n = (R >> 4) & 3, rr = R & 15;
+    const int wrow = (n < 2 ? 0 : I) + cb * kBlock + 32 * g + 16 * (n & 1) + rr;
+    boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ bg_key(R)) * 16);
+  }
+  const uint32_t soff = 4u * (uint32_t)pl.perm_token[rm.src(64 * (wave & 1) + lane)];
+  const uint8_t* wbase = pb.w13 + (size_t)e * 2 * I * H;
+  auto issue = [&](int j) {
+    const int k = min(j, KB - 1);
+    const uint32_t st = ring_lds + (uint32_t)((j % kBgStages) * kBgStage);
+    const uint8_t* abase = pb.hidden + (size_t)k * kBlock;
+    const uint8_t* bbase = wbase + (size_t)k * kBlock;
+    const float* sbase = pb.hscale + (size_t)k * T;
+#pragma unroll
+    for (int q = 0; q < 2; q++) dma_lds16_s(aoff[q], abase, st + (16 * wave + 8 * q) * 128);
+#pragma unroll
+    for (int q = 0; q < 4; q++) dma_lds16_s(boff[q], bbase, st + kBgA + (32 * wave + 8 * q) * 128);
+    // wavefronts 2..7 repeat the row scales of 0 and 1 (same bytes), so that every wavefront
+    // issues the same operations
+    dma_lds4_s(soff, sbase, st + kBgA + kBgB + (wave & 1) * 256);
+  };
+
+  // the table and scale loads of the unit are complete: only DMAs count from here
+  MOEFP8_WAIT_VMCNT(0);
+  for (int d = 0; d < kBgStages - 1; d++) issue(d);
+  v4f acc[NT][4];
+#pragma unroll
+  for (int i = 0; i < NT; i++)
+#pragma unroll
+    for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  for (int j = 0; j < KB; j++) {
+    // stage j's DMAs are done once only the following stage's (7 per wavefront) may be in flight
+    static_assert((kBgStages - 2) * kBgOps == 7, "wait count");
+    MOEFP8_WAIT_VMCNT(7);
+    barrier_lds();
+    const uint8_t* st = ring + (j % kBgStages) * kBgStage;
+    v8i B[4];
+#pragma unroll
+    for (int n = 0; n < 4; n++) {
+      const uint8_t* bt = st + kBgA + (64 * wn + 16 * n) * 128;
+      B[n] = cat(*reinterpret_cast<const v4i*>(bt + rd0), *reinterpret_cast<const v4i*>(bt + rd1));
+    }
+    const float2 sw = sw_s[j];
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+      const int t = tile(i);
+      const uint8_t* at = st + t * 16 * 128;
+      const v8i a = cat(*reinterpret_cast<const v4i*>(at + rd0), *reinterpret_cast<const v4i*>(at + rd1));
+      const float4 sa = *reinterpret_cast<const float4*>(st + kBgA + kBgB + (16 * t + 4 * kg) * 4);
+      const float4 su = {sa.x * sw.x, sa.y * sw.x, sa.z * sw.x, sa.w * sw.x};
+      const float4 sg = {sa.x * sw.y, sa.y * sw.y, sa.z * sw.y, sa.w * sw.y};
+      v8h a16[4];
+      if (i >= NF) widen_fp8_operand(a, a16);
+#pragma unroll
+      for (int n = 0; n < 4; n++) {
+        const float4 sc = n < 2 ? su : sg;
+        v4f p;
+        if (i >= NF) {
+          v8h b16[4];
+          widen_fp8_operand(B[n], b16);
+          p = mfma_f16_block(a16, b16, v4f{0.f, 0.f, 0.f, 0.f});
+        } else {
+          p = mfma16x16x128(a, B[n], v4f{0.f, 0.f, 0.f, 0.f});
+        }
+        acc[i][n][0] += p[0] * sc.x;
+        acc[i][n][1] += p[1] * sc.y;
+        acc[i][n][2] += p[2] * sc.z;
+        acc[i][n][3] += p[3] * sc.w;
+      }
+    }
+    // stage (j + 2) % 3 was last read at step j - 1, before this step's barrier
+    issue(j + kBgStages - 1);
+  }
+  MOEFP8_WAIT_VMCNT(0);
+  // the workgroup's next unit, claimed now so that the atomic overlaps the epilogue
+  if (threadIdx.x == 0) *next_s = grab_unit(pl.queues, n_units);
+
+  // epilogue: C = silu(gate) * up, per-row max over the unit's 128 columns, hi/lo split
+  const int col0 = cb * kBlock + 32 * wn;
+  float c[NT][2][4];
+#pragma unroll
+  for (int i = 0; i < NT; i++)
+#pragma unroll
+    for (int jn = 0; jn < 2; jn++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) c[i][jn][r] = silu_f32(acc[i][jn + 2][r]) * acc[i][jn][r];
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const int t = tile(i);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float m = fmaxf(fabsf(c[i][0][r]), fabsf(c[i][1][r]));
+      m = fmaxf(m, dpp_f32<kDppXor1>(m));
+      m = fmaxf(m, dpp_f32<kDppXor2>(m));
+      m = fmaxf(m, dpp_f32<kDppHalfMirror>(m));
+      m = fmaxf(m, dpp_f32<kDppRowMirror>(m));
+      if (lr == 0) amax_s[wn][16 * t + 4 * kg + r] = m;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const int t = tile(i);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int R = 16 * t + 4 * kg + r;
+      if (!rm.valid(R)) continue;
+      const float amax = fmaxf(fmaxf(amax_s[0][R], amax_s[1][R]), fmaxf(amax_s[2][R], amax_s[3][R]));
+      float inv, scale;
+      split_scale(amax, inv, scale);
+      const size_t p = (size_t)rm.src(R);
+      const bool exact_row = R >= rm.xfrom;
+#pragma unroll
+      for (int jn = 0; jn < 2; jn++) {
+        const int col = col0 + 16 * jn + lr;
+        const float v = fminf(fmaxf(c[i][jn][r] * inv, -448.0f), 448.0f);
+        const _Float16 hi = (_Float16)v;
+        ch.hi[p * I + col] = hi;
+        if (exact_row) ch.lo16[p * I + col] = (_Float16)(v - (float)hi);
+        else if (two)   // GEMM2 reads it in blocks holding class 1 rows
+          ch.lo[p * I + col] = (uint8_t)f32_to_e4m3(fminf(fmaxf((v - (float)hi) * kLoScale, -448.0f), 448.0f));
+      }
+      if (wn == 0 && lr == 0) ch.scale[p * NCB + cb] = scale;
+    }
+  }
+}
+
+// Units (m-block, 128 C columns) over the blocks (128-row class 0/1 blocks, mixed blocks and
+// 32-row exact-product blocks).
 __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Plan pl, CHalf8 ch) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kBgStages * kBgStage];
   __shared__ __attribute__((aligned(16))) float2 sw_s[kBigMaxKB];
@@ -636,12 +833,34 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Pl
       if (t < KB) sw_s[t] = float2{su[t], sg[t]};
     }
     __syncthreads();
-#define MOEFP8_G1_UNIT(NT, EXACT) \
+    const RowMap rm = row_map(row0, rows, flags);
+    const bool two = (flags & kFlagTwoTermC) != 0;
+    const int wm = wave_index() & 1;
+#define MOEFP8_G1_UNIT(NF, NX, TF0, TX0) \
+  gemm1_big_mixed_unit<NF, NX>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, rm, cb, two, TF0, TX0, &next_s, n_units)
+    if (flags & kFlagMixed) {
+      const TileSplit ts = mixed_split(rm, wm);
+      const int nf = uniform(ts.nf), tf0 = uniform(ts.tf0), tx0 = uniform(ts.tx0);
+      if (ts.nx == 0) {
+        if (nf == 1) MOEFP8_G1_UNIT(1, 0, tf0, 0);
+        else if (nf == 2) MOEFP8_G1_UNIT(2, 0, tf0, 0);
+        else if (nf == 3) MOEFP8_G1_UNIT(3, 0, tf0, 0);
+        else MOEFP8_G1_UNIT(4, 0, tf0, 0);
+      } else {
+        if (nf == 0) MOEFP8_G1_UNIT(0, 1, 0, tx0);
+        else if (nf == 1) MOEFP8_G1_UNIT(1, 1, tf0, tx0);
+        else if (nf == 2) MOEFP8_G1_UNIT(2, 1, tf0, tx0);
+        else MOEFP8_G1_UNIT(3, 1, tf0, tx0);
+      }
+    } else {
+#define MOEFP8_G1_REG(NT, EXACT) \
   gemm1_big_unit<NT, EXACT>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags, &next_s, n_units)
-    if (flags & kFlagExactProducts) MOEFP8_G1_UNIT(1, true);
-    else if (rows <= 32) MOEFP8_G1_UNIT(1, false);
-    else if (rows <= 64) MOEFP8_G1_UNIT(2, false);
-    else MOEFP8_G1_UNIT(4, false);
+      if (flags & kFlagExactProducts) MOEFP8_G1_REG(1, true);
+      else if (rows <= 32) MOEFP8_G1_REG(1, false);
+      else if (rows <= 64) MOEFP8_G1_REG(2, false);
+      else MOEFP8_G1_REG(4, false);
+#undef MOEFP8_G1_REG
+    }
 #undef MOEFP8_G1_UNIT
     // next_s is written
     __syncthreads();
@@ -873,11 +1092,13 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
 // two 32-K MFMAs t = 0, 1 (the same order for both operands): its W2 and lo bytes are one
 // 16-byte chunk, its hi values two.
 //
-// LDS stage: hi [128 rows][128 B] (chunks swizzled by bg_key), lo [128 rows][64 B] and W2
-// [256 rows][64 B] (chunk c of row r in slot c ^ bg_key4(r)), 128 row scales of C.
+// LDS stage: hi [128 rows][128 B] (chunks swizzled by bg_key), e4m3 lo [128 rows][64 B], f16 lo
+// of up to 32 exact-product rows [32 rows][128 B] (bg_key), W2 [256 rows][64 B] (chunk c of row r
+// in slot c ^ bg_key4(r)), 128 row scales of C.
 constexpr int kB2Cols = 256;
 constexpr int kB2Hi = kBgRows * 128;
-constexpr int kB2Lo = kBgRows * 64;
+constexpr int kB2LoE = kBgRows * 64;
+constexpr int kB2Lo = kB2LoE + 32 * 128;
 constexpr int kB2W = kB2Cols * 64;
 constexpr int kB2Stage = kB2Hi + kB2Lo + kB2W + kBgRows * 4;
 constexpr int kB2Stages = 3;
@@ -902,45 +1123,49 @@ __device__ __forceinline__ void widen16(const v4i& x, float scale, v8h& t0, v8h&
   }
 }
 
-// One unit.  Wavefront (wm, wn) computes m-tiles NT wm .. NT wm + NT - 1 (NT = 4, 2 or 1 for
-// blocks of more than 64, 33..64 and at most 32 rows).  kMode: kOneTerm / kTwoTerms, kPrecise
-// (blocks of at most 32 exact-product rows, NT = 1, with C's hi and f16 lo terms, the lo rows
-// staged in the stage's lo region as [32 rows][128 B]).
-template <int kMode, int NT>
+// One unit.  The block's DMAs: C's hi rows, its e4m3 lo rows (kLoE: blocks holding class 1
+// rows), its f16 lo rows of the exact-product rows (kLo16: exact-product and mixed blocks), W2 and
+// the row scales.  This wavefront computes NF m-tiles tf0 .. from hi (+ the e4m3 lo term when
+// kLoE) and NX m-tiles tx0 .. from hi + the f16 lo term, as in GEMM1: wavefront (wm, wn) of a
+// regular block takes 4, 2 or 1 tiles by block height, of an exact-product block tile wm, of a
+// mixed block its half of the tiles (mixed_split).
+template <bool kLoE, bool kLo16, int NF, int NX>
 __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
-                                               uint32_t ring_lds, const float* sw2_s, int e, int row0, int rows,
-                                               int hc, float* __restrict__ obuf, int* queues, int* next_s,
-                                               int n_units) {
-  static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
-  static_assert(kMode != kPrecise || NT == 1, "exact-product blocks hold at most 32 rows");
+                                               uint32_t ring_lds, const float* sw2_s, int e, const RowMap& rm,
+                                               int hc, int tf0, int tx0, float* __restrict__ obuf, int* queues,
+                                               int* next_s, int n_units) {
+  constexpr int NT = NF + NX;
+  static_assert(NT >= 1 && NT <= 4, "m-tiles per wavefront");
+  static_assert(NX == 0 || kLo16, "exact-product tiles need the f16 lo rows");
+  constexpr int kOps = 2 + (kLoE ? 1 : 0) + (kLo16 ? 1 : 0) + 2 + 1;   // DMAs per wavefront and stage
   const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
   const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wn = wave >> 1;
+  auto tile = [&](int i) { return i < NF ? tf0 + i : tx0 + (i - NF); };
   // DMA sources (per-lane byte offsets): hi rows 16w + 8q + (lane / 8), 8 slots per row; e4m3 lo
   // rows 16w + (lane / 4), W2 rows 32w + 16q + (lane / 4), 4 slots per row; f16 lo rows
-  // 8 (w % 4) + (lane / 8); row scales 64 (w % 2) + lane
-  uint32_t hoff[2], loff = 0, woff[2];
+  // xfrom + 8 (w % 4) + (lane / 8); row scales 64 (w % 2) + lane
+  uint32_t hoff[2], loff = 0, xoff = 0, woff[2];
 #pragma unroll
   for (int q = 0; q < 2; q++) {
     const int r = 16 * wave + 8 * q + (lane >> 3);
-    const int p = row0 + min(r, rows - 1);
-    hoff[q] = (uint32_t)p * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
+    hoff[q] = (uint32_t)rm.src(r) * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
   }
-  if (kMode == kTwoTerms) {
+  if (kLoE) {
     const int r = 16 * wave + (lane >> 2);
-    const int p = row0 + min(r, rows - 1);
-    loff = (uint32_t)p * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(r))) * 16);
-  } else if (kMode == kPrecise) {
-    const int r = 8 * (wave & 3) + (lane >> 3);
-    const int p = row0 + min(r, rows - 1);
-    loff = (uint32_t)p * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
+    loff = (uint32_t)rm.src(r) * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(r))) * 16);
+  }
+  if (kLo16) {
+    const int i = 8 * (wave & 3) + (lane >> 3);
+    xoff = (uint32_t)rm.src(min(rm.xfrom + i, kBgRows - 1)) * (uint32_t)(2 * I) +
+           (uint32_t)((((lane & 7) ^ bg_key(i))) * 16);
   }
 #pragma unroll
   for (int q = 0; q < 2; q++) {
     const int R = 32 * wave + 16 * q + (lane >> 2);
     woff[q] = (uint32_t)(hc * kB2Cols + R) * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(R))) * 16);
   }
-  const uint32_t soff = 4u * (uint32_t)((row0 + min(64 * (wave & 1) + lane, rows - 1)) * KB);
+  const uint32_t soff = 4u * (uint32_t)(rm.src(64 * (wave & 1) + lane) * KB);
   const uint8_t* wbase = pb.w2 + (size_t)e * H * I;
   auto issue = [&](int j) {
     const int k = min(j, KS - 1);
@@ -948,11 +1173,13 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
     const uint8_t* hbase = reinterpret_cast<const uint8_t*>(ch.hi) + (size_t)k * 128;
 #pragma unroll
     for (int q = 0; q < 2; q++) dma_lds16_s(hoff[q], hbase, st + (16 * wave + 8 * q) * 128);
-    if (kMode == kTwoTerms) dma_lds16_s(loff, ch.lo + (size_t)k * 64, st + kB2Hi + 16 * wave * 64);
-    if (kMode == kPrecise)
-      dma_lds16_s(loff, reinterpret_cast<const uint8_t*>(ch.lo16) + (size_t)k * 128, st + kB2Hi + 8 * (wave & 3) * 128);
+    if (kLoE) dma_lds16_s(loff, ch.lo + (size_t)k * 64, st + kB2Hi + 16 * wave * 64);
+    if (kLo16)
+      dma_lds16_s(xoff, reinterpret_cast<const uint8_t*>(ch.lo16) + (size_t)k * 128,
+                  st + kB2Hi + kB2LoE + 8 * (wave & 3) * 128);
 #pragma unroll
-    for (int q = 0; q < 2; q++) dma_lds16_s(woff[q], wbase + (size_t)k * 64, st + kB2Hi + kB2Lo + (32 * wave + 16 * q) * 64);
+    for (int q = 0; q < 2; q++)
+      dma_lds16_s(woff[q], wbase + (size_t)k * 64, st + kB2Hi + kB2Lo + (32 * wave + 16 * q) * 64);
     dma_lds4_s(soff, ch.scale + k / 2, st + kB2Hi + kB2Lo + kB2W + (wave & 1) * 256);
   };
   // operand read offsets: hi (and f16 lo) chunks 2kg + t of row lr (bg_key), e4m3 lo / W2 chunk kg
@@ -969,10 +1196,12 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
 #pragma unroll
     for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < KS; j++) {
-    // one stage in flight past the current one: 5 (one term) or 6 operations per wavefront
+    // one stage in flight past the current one: kOps operations per wavefront
     static_assert(kB2Stages == 3, "wait count");
-    if (kMode == kOneTerm) MOEFP8_WAIT_VMCNT(5);
-    else MOEFP8_WAIT_VMCNT(6);
+    static_assert(kOps >= 5 && kOps <= 7, "wait count");
+    if constexpr (kOps == 5) MOEFP8_WAIT_VMCNT(5);
+    else if constexpr (kOps == 6) MOEFP8_WAIT_VMCNT(6);
+    else MOEFP8_WAIT_VMCNT(7);
     barrier_lds();
     const uint8_t* st = ring + (j % kB2Stages) * kB2Stage;
     v8h b16[4][2];
@@ -983,15 +1212,16 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
     const float sw = sw2_s[(j / 2) * 2 + (wn >> 1)];
 #pragma unroll
     for (int i = 0; i < NT; i++) {
-      const int t = NT * wm + i;
+      const int t = tile(i);
       const uint8_t* ht = st + t * 16 * 128;
       const v8h a0 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh0));
       const v8h a1 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh1));
       v8h l0 = {}, l1 = {};
-      if constexpr (kMode == kTwoTerms)
+      const bool lo_term = i >= NF || kLoE;
+      if (i < NF && kLoE)
         widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + t * 16 * 64 + rq), 1.0f / kLoScale, l0, l1);
-      if constexpr (kMode == kPrecise) {
-        const uint8_t* lt = st + kB2Hi + t * 16 * 128;
+      if (i >= NF) {
+        const uint8_t* lt = st + kB2Hi + kB2LoE + (16 * t - rm.xfrom) * 128;
         l0 = as_v8h(*reinterpret_cast<const v4i*>(lt + rh0));
         l1 = as_v8h(*reinterpret_cast<const v4i*>(lt + rh1));
       }
@@ -1001,7 +1231,7 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
       for (int n = 0; n < 4; n++) {
         v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b16[n][0], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b16[n][1], p, 0, 0, 0);
-        if constexpr (kMode != kOneTerm) {
+        if (lo_term) {
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, b16[n][0], p, 0, 0, 0);
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, b16[n][1], p, 0, 0, 0);
         }
@@ -1018,12 +1248,12 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
   if (threadIdx.x == 0) *next_s = grab_unit(queues, n_units);
 #pragma unroll
   for (int i = 0; i < NT; i++) {
-    const int t = NT * wm + i;
+    const int t = tile(i);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const int row = 16 * t + 4 * kg + r;
-      if (row < rows) {
-        const int p = row0 + row;
+      const int R = 16 * t + 4 * kg + r;
+      if (rm.valid(R)) {
+        const int p = rm.src(R);
         const float w = pl.perm_w[p];
 #pragma unroll
         for (int n = 0; n < 4; n++) obuf[(size_t)p * H + hc * kB2Cols + 64 * wn + 16 * n + lr] = acc[i][n][r] * w;
@@ -1057,17 +1287,41 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
       if (t < 2 * KB) sw2_s[t] = pb.s2[((size_t)e * HB + 2 * hc + (t & 1)) * KB + (t >> 1)];
     }
     __syncthreads();
-#define MOEFP8_G2_UNIT(MODE, NT) \
-  gemm2_big_unit<MODE, NT>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf, queues, &next_s, n_units)
-    if (flags & kFlagExactProducts) MOEFP8_G2_UNIT(kPrecise, 1);
+    const RowMap rm = row_map(row0, rows, flags);
+    const int wm = wave_index() & 1;
+#define MOEFP8_G2_UNIT(LOE, LO16, NF, NX, TF0, TX0)                                                          \
+  gemm2_big_unit<LOE, LO16, NF, NX>(pb, pl, ch, ring, ring_lds, sw2_s, e, rm, hc, TF0, TX0, obuf, queues, &next_s, \
+                                    n_units)
+    if (flags & kFlagMixed) {
+      const TileSplit ts = mixed_split(rm, wm);
+      const int nf = uniform(ts.nf), tf0 = uniform(ts.tf0), tx0 = uniform(ts.tx0);
+#define MOEFP8_G2_MIXED(LOE)                                      \
+  if (ts.nx == 0) {                                               \
+    if (nf == 1) MOEFP8_G2_UNIT(LOE, true, 1, 0, tf0, 0);         \
+    else if (nf == 2) MOEFP8_G2_UNIT(LOE, true, 2, 0, tf0, 0);    \
+    else if (nf == 3) MOEFP8_G2_UNIT(LOE, true, 3, 0, tf0, 0);    \
+    else MOEFP8_G2_UNIT(LOE, true, 4, 0, tf0, 0);                 \
+  } else {                                                        \
+    if (nf == 0) MOEFP8_G2_UNIT(LOE, true, 0, 1, 0, tx0);         \
+    else if (nf == 1) MOEFP8_G2_UNIT(LOE, true, 1, 1, tf0, tx0);  \
+    else if (nf == 2) MOEFP8_G2_UNIT(LOE, true, 2, 1, tf0, tx0);  \
+    else MOEFP8_G2_UNIT(LOE, true, 3, 1, tf0, tx0);               \
+  }
+      if (flags & kFlagTwoTermC) {
+        MOEFP8_G2_MIXED(true)
+      } else {
+        MOEFP8_G2_MIXED(false)
+      }
+#undef MOEFP8_G2_MIXED
+    } else if (flags & kFlagExactProducts) MOEFP8_G2_UNIT(false, true, 0, 1, 0, wm);
     else if (flags & kFlagTwoTermC) {
-      if (rows <= 32) MOEFP8_G2_UNIT(kTwoTerms, 1);
-      else if (rows <= 64) MOEFP8_G2_UNIT(kTwoTerms, 2);
-      else MOEFP8_G2_UNIT(kTwoTerms, 4);
+      if (rows <= 32) MOEFP8_G2_UNIT(true, false, 1, 0, wm, 0);
+      else if (rows <= 64) MOEFP8_G2_UNIT(true, false, 2, 0, 2 * wm, 0);
+      else MOEFP8_G2_UNIT(true, false, 4, 0, 4 * wm, 0);
     } else {
-      if (rows <= 32) MOEFP8_G2_UNIT(kOneTerm, 1);
-      else if (rows <= 64) MOEFP8_G2_UNIT(kOneTerm, 2);
-      else MOEFP8_G2_UNIT(kOneTerm, 4);
+      if (rows <= 32) MOEFP8_G2_UNIT(false, false, 1, 0, wm, 0);
+      else if (rows <= 64) MOEFP8_G2_UNIT(false, false, 2, 0, 2 * wm, 0);
+      else MOEFP8_G2_UNIT(false, false, 4, 0, 4 * wm, 0);
     }
 #undef MOEFP8_G2_UNIT
     // next_s is written

@@ -373,6 +373,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pa.mblocks = reinterpret_cast<int4*>(ws + L.mblocks);
   pa.mbgroup = reinterpret_cast<int2*>(ws + L.mbgroup);
   pa.queues = reinterpret_cast<int*>(ws + L.queues);
+  pa.mixed = large_big(T, H, I) ? 1 : 0;   // the 128-row GEMMs run mixed blocks
   pa.rows_a = large_rows_a(T, H, I);
   pa.rows_b = large_rows_b(T, H, I);
   pl.canon_token = pa.canon_token;

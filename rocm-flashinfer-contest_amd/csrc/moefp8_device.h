@@ -77,6 +77,10 @@ constexpr float kPreciseRms = 96.0f;
 constexpr float kOneTermRms = 8.0f;
 constexpr uint8_t kFlagExactProducts = 1;
 constexpr uint8_t kFlagTwoTermC = 2;
+// Large-T m-block flags only: the block also holds its expert's <= 32 exact-product rows, their
+// count in the bits from kMixedShift up.
+constexpr int kFlagMixed = 4;
+constexpr int kMixedShift = 8;
 
 __device__ __forceinline__ float predicted_output_rms(float a2, float w, float s13, float s2, float sqrt_i) {
   return fabsf(w) * 0.7f * a2 * s13 * s13 * s2 * sqrt_i;

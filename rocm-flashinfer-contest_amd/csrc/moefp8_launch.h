@@ -124,6 +124,7 @@ struct LargePermArgs {
   int4* mblocks;        // m-blocks of both GEMMs {expert, first row, rows, flags}
   int2* mbgroup;        // per m-block: {first m-block of its expert, the expert's m-blocks}
   int* queues;          // [kUnitQueues * kQueueStride] unit queues of the grouped GEMMs, zeroed here
+  int mixed;            // fold <= 32 exact-product rows into the expert's last class 0/1 block
   int rows_a;           // block height over an expert's class 0 and 1 rows
   int rows_b;           // block height over its class 2 (exact-product) rows
 };

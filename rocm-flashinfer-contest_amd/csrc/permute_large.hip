@@ -32,6 +32,15 @@ __device__ __forceinline__ uint8_t class_flags(int c) {
   return c == 0 ? 0 : (c == 1 ? kFlagTwoTermC : (uint8_t)(kFlagTwoTermC | kFlagExactProducts));
 }
 
+// Does an expert with n01 class 0/1 rows and n2 exact-product rows fold the latter into its last
+// class 0/1 block (a mixed block: the exact rows take the block's last ceil(n2 / 16) m-tiles)?
+// Only with 128-row blocks, at most 32 exact rows and room for them.
+__device__ __forceinline__ bool folds_exact(const LargePermArgs& a, int n01, int n2) {
+  if (!a.mixed || n2 < 1 || n2 > 32 || n01 < 1) return false;
+  const int last = n01 - (n01 - 1) / a.rows_a * a.rows_a;
+  return last <= a.rows_a - 16 * ((n2 + 15) / 16);
+}
+
 // Bucket of slot k of token t, or -1 if the expert is not local.
 __device__ __forceinline__ int pair_bucket(const LargePermArgs& a, int t, int k, float a2, float* w_out, int* le_out) {
   const int le = a.topk_ids[(size_t)t * kTopK + k] - a.offset;
@@ -116,7 +125,9 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
   __syncthreads();
   // expert offsets, 16-row m-tile offsets and m-block offsets, expert by expert: blocks of rows_a
   // rows over an expert's class 0 and 1 rows (two-term C in the blocks that hold class 1 rows),
-  // then blocks of rows_b rows over its class 2 rows; both GEMMs run this one table (GEMM2 on
+  // then blocks of rows_b rows over its class 2 rows, or those folded into its last class 0/1
+  // block (folds_exact: 27 of 107 blocks at T = 8192 held <= 32 exact rows each, a quarter of the
+  // GEMMs' weight streams for 5% of the rows); both GEMMs run this one table (GEMM2 on
   // separate class 0 and class 1 blocks had 11% more blocks, hence more weight streams, and was
   // 4% slower at T = 8192).  An expert's blocks are consecutive, so the units that stream its
   // weights run close together in time and share them through L2.
@@ -127,8 +138,9 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
       const int n0 = e < E ? tot[kClasses * e] : 0, n1 = e < E ? tot[kClasses * e + 1] : 0;
       const int n2 = e < E ? tot[kClasses * e + 2] : 0, n = n0 + n1 + n2;
       const int mt = (n + 15) / 16;
-      const int bx = (n2 + a.rows_b - 1) / a.rows_b;
-      const int b1 = (n0 + n1 + a.rows_a - 1) / a.rows_a + bx;
+      const int ba = (n0 + n1 + a.rows_a - 1) / a.rows_a;
+      const int bx = folds_exact(a, n0 + n1, n2) ? 0 : (n2 + a.rows_b - 1) / a.rows_b;
+      const int b1 = ba + bx;
       const int pn = wave_exclusive_sum(n), pmt = wave_exclusive_sum(mt);
       const int p1 = wave_exclusive_sum(b1);
       const uint64_t act = __ballot(n > 0);
@@ -175,7 +187,9 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
     const int ba = (c01 + a.rows_a - 1) / a.rows_a;
     if (j < ba) {
       const int r0 = j * a.rows_a, rows = min(a.rows_a, c01 - r0);
-      a.mblocks[g] = int4{e, eoff[e] + r0, rows, r0 + rows > c0 ? (int)class_flags(1) : 0};
+      int flags = r0 + rows > c0 ? (int)class_flags(1) : 0;
+      if (j == ba - 1 && folds_exact(a, c01, n - c01)) flags |= kFlagMixed | ((n - c01) << kMixedShift);
+      a.mblocks[g] = int4{e, eoff[e] + r0, rows, flags};
     } else {
       const int r0 = c01 + (j - ba) * a.rows_b;
       a.mblocks[g] = int4{e, eoff[e] + r0, min(a.rows_b, n - r0), (int)class_flags(2)};
