@@ -1123,14 +1123,143 @@ __device__ __forceinline__ void widen16(const v4i& x, float scale, v8h& t0, v8h&
   }
 }
 
-// One unit.  The block's DMAs: C's hi rows, its e4m3 lo rows (kLoE: blocks holding class 1
-// rows), its f16 lo rows of the exact-product rows (kLo16: exact-product and mixed blocks), W2 and
-// the row scales.  This wavefront computes NF m-tiles tf0 .. from hi (+ the e4m3 lo term when
-// kLoE) and NX m-tiles tx0 .. from hi + the f16 lo term, as in GEMM1: wavefront (wm, wn) of a
-// regular block takes 4, 2 or 1 tiles by block height, of an exact-product block tile wm, of a
-// mixed block its half of the tiles (mixed_split).
-template <bool kLoE, bool kLo16, int NF, int NX>
+// One unit.  Wavefront (wm, wn) computes m-tiles NT wm .. NT wm + NT - 1 (NT = 4, 2 or 1 for
+// blocks of more than 64, 33..64 and at most 32 rows).  kMode: kOneTerm / kTwoTerms, kPrecise
+// (blocks of at most 32 exact-product rows, NT = 1, with C's hi and f16 lo terms, the lo rows
+// staged in the stage's lo region as [32 rows][128 B]).
+template <int kMode, int NT>
 __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
+                                               uint32_t ring_lds, const float* sw2_s, int e, int row0, int rows,
+                                               int hc, float* __restrict__ obuf, int* queues, int* next_s,
+                                               int n_units) {
+  static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
+  static_assert(kMode != kPrecise || NT == 1, "exact-product blocks hold at most 32 rows");
+  const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
+  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+  // DMA sources (per-lane byte offsets): hi rows 16w + 8q + (lane / 8), 8 slots per row; e4m3 lo
+  // rows 16w + (lane / 4), W2 rows 32w + 16q + (lane / 4), 4 slots per row; f16 lo rows
+  // 8 (w % 4) + (lane / 8); row scales 64 (w % 2) + lane
+  uint32_t hoff[2], loff = 0, woff[2];
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int r = 16 * wave + 8 * q + (lane >> 3);
+    const int p = row0 + min(r, rows - 1);
+    hoff[q] = (uint32_t)p * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
+  }
+  if (kMode == kTwoTerms) {
+    const int r = 16 * wave + (lane >> 2);
+    const int p = row0 + min(r, rows - 1);
+    loff = (uint32_t)p * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(r))) * 16);
+  } else if (kMode == kPrecise) {
+    const int r = 8 * (wave & 3) + (lane >> 3);
+    const int p = row0 + min(r, rows - 1);
+    loff = (uint32_t)p * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int R = 32 * wave + 16 * q + (lane >> 2);
+    woff[q] = (uint32_t)(hc * kB2Cols + R) * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(R))) * 16);
+  }
+  const uint32_t soff = 4u * (uint32_t)((row0 + min(64 * (wave & 1) + lane, rows - 1)) * KB);
+  const uint8_t* wbase = pb.w2 + (size_t)e * H * I;
+  auto issue = [&](int j) {
+    const int k = min(j, KS - 1);
+    const uint32_t st = ring_lds + (uint32_t)((j % kB2Stages) * kB2Stage);
+    const uint8_t* hbase = reinterpret_cast<const uint8_t*>(ch.hi) + (size_t)k * 128;
+#pragma unroll
+    for (int q = 0; q < 2; q++) dma_lds16_s(hoff[q], hbase, st + (16 * wave + 8 * q) * 128);
+    if (kMode == kTwoTerms) dma_lds16_s(loff, ch.lo + (size_t)k * 64, st + kB2Hi + 16 * wave * 64);
+    if (kMode == kPrecise)
+      dma_lds16_s(loff, reinterpret_cast<const uint8_t*>(ch.lo16) + (size_t)k * 128, st + kB2Hi + 8 * (wave & 3) * 128);
+#pragma unroll
+    for (int q = 0; q < 2; q++) dma_lds16_s(woff[q], wbase + (size_t)k * 64, st + kB2Hi + kB2Lo + (32 * wave + 16 * q) * 64);
+    dma_lds4_s(soff, ch.scale + k / 2, st + kB2Hi + kB2Lo + kB2W + (wave & 1) * 256);
+  };
+  // operand read offsets: hi (and f16 lo) chunks 2kg + t of row lr (bg_key), e4m3 lo / W2 chunk kg
+  // of row lr (bg_key4)
+  const int rh0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
+  const int rh1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
+  const int rq = lr * 64 + ((kg ^ bg_key4(lr)) * 16);
+
+  MOEFP8_WAIT_VMCNT(0);
+  for (int d = 0; d < kB2Stages - 1; d++) issue(d);
+  v4f acc[NT][4];
+#pragma unroll
+  for (int i = 0; i < NT; i++)
+#pragma unroll
+    for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < KS; j++) {
+    // one stage in flight past the current one: 5 (one term) or 6 operations per wavefront
+    static_assert(kB2Stages == 3, "wait count");
+    if (kMode == kOneTerm) MOEFP8_WAIT_VMCNT(5);
+    else MOEFP8_WAIT_VMCNT(6);
+    barrier_lds();
+    const uint8_t* st = ring + (j % kB2Stages) * kB2Stage;
+    v8h b16[4][2];
+#pragma unroll
+    for (int n = 0; n < 4; n++)
+      widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + kB2Lo + (64 * wn + 16 * n) * 64 + rq), 1.0f, b16[n][0],
+              b16[n][1]);
+    const float sw = sw2_s[(j / 2) * 2 + (wn >> 1)];
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+      const int t = NT * wm + i;
+      const uint8_t* ht = st + t * 16 * 128;
+      const v8h a0 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh0));
+      const v8h a1 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh1));
+      v8h l0 = {}, l1 = {};
+      if constexpr (kMode == kTwoTerms)
+        widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + t * 16 * 64 + rq), 1.0f / kLoScale, l0, l1);
+      if constexpr (kMode == kPrecise) {
+        const uint8_t* lt = st + kB2Hi + t * 16 * 128;
+        l0 = as_v8h(*reinterpret_cast<const v4i*>(lt + rh0));
+        l1 = as_v8h(*reinterpret_cast<const v4i*>(lt + rh1));
+      }
+      const float4 sa = *reinterpret_cast<const float4*>(st + kB2Hi + kB2Lo + kB2W + (16 * t + 4 * kg) * 4);
+      const float4 sc = {sa.x * sw, sa.y * sw, sa.z * sw, sa.w * sw};
+#pragma unroll
+      for (int n = 0; n < 4; n++) {
+        v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b16[n][0], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b16[n][1], p, 0, 0, 0);
+        if constexpr (kMode != kOneTerm) {
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, b16[n][0], p, 0, 0, 0);
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, b16[n][1], p, 0, 0, 0);
+        }
+        acc[i][n][0] += p[0] * sc.x;
+        acc[i][n][1] += p[1] * sc.y;
+        acc[i][n][2] += p[2] * sc.z;
+        acc[i][n][3] += p[3] * sc.w;
+      }
+    }
+    issue(j + kB2Stages - 1);
+  }
+  MOEFP8_WAIT_VMCNT(0);
+  // the workgroup's next unit, claimed now so that the atomic overlaps the epilogue
+  if (threadIdx.x == 0) *next_s = grab_unit(queues, n_units);
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const int t = NT * wm + i;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int row = 16 * t + 4 * kg + r;
+      if (row < rows) {
+        const int p = row0 + row;
+        const float w = pl.perm_w[p];
+#pragma unroll
+        for (int n = 0; n < 4; n++) obuf[(size_t)p * H + hc * kB2Cols + 64 * wn + 16 * n + lr] = acc[i][n][r] * w;
+      }
+    }
+  }
+}
+
+// One unit of a mixed block.  Its DMAs: C's hi rows, its e4m3 lo rows (kLoE: the block holds class
+// 1 rows), the f16 lo rows of its exact-product rows (staged after the e4m3 ones), W2 and the row
+// scales.  This wavefront computes NF m-tiles tf0 .. from hi (+ the e4m3 lo term when kLoE) and NX
+// m-tiles tx0 .. from hi + the f16 lo term, its half of the block's tiles (mixed_split).  (Kept
+// apart from gemm2_big_unit, whose K loop the compiler schedules worse in this general form.)
+template <bool kLoE, bool kLo16, int NF, int NX>
+__device__ __forceinline__ void gemm2_big_mixed_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float* sw2_s, int e, const RowMap& rm,
                                                int hc, int tf0, int tx0, float* __restrict__ obuf, int* queues,
                                                int* next_s, int n_units) {
@@ -1289,9 +1418,11 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
     __syncthreads();
     const RowMap rm = row_map(row0, rows, flags);
     const int wm = wave_index() & 1;
-#define MOEFP8_G2_UNIT(LOE, LO16, NF, NX, TF0, TX0)                                                          \
-  gemm2_big_unit<LOE, LO16, NF, NX>(pb, pl, ch, ring, ring_lds, sw2_s, e, rm, hc, TF0, TX0, obuf, queues, &next_s, \
-                                    n_units)
+#define MOEFP8_G2_UNIT(LOE, LO16, NF, NX, TF0, TX0)                                                         \
+  gemm2_big_mixed_unit<LOE, LO16, NF, NX>(pb, pl, ch, ring, ring_lds, sw2_s, e, rm, hc, TF0, TX0, obuf, queues, \
+                                          &next_s, n_units)
+#define MOEFP8_G2_REG(MODE, NT) \
+  gemm2_big_unit<MODE, NT>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf, queues, &next_s, n_units)
     if (flags & kFlagMixed) {
       const TileSplit ts = mixed_split(rm, wm);
       const int nf = uniform(ts.nf), tf0 = uniform(ts.tf0), tx0 = uniform(ts.tx0);
@@ -1313,16 +1444,17 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
         MOEFP8_G2_MIXED(false)
       }
 #undef MOEFP8_G2_MIXED
-    } else if (flags & kFlagExactProducts) MOEFP8_G2_UNIT(false, true, 0, 1, 0, wm);
+    } else if (flags & kFlagExactProducts) MOEFP8_G2_REG(kPrecise, 1);
     else if (flags & kFlagTwoTermC) {
-      if (rows <= 32) MOEFP8_G2_UNIT(true, false, 1, 0, wm, 0);
-      else if (rows <= 64) MOEFP8_G2_UNIT(true, false, 2, 0, 2 * wm, 0);
-      else MOEFP8_G2_UNIT(true, false, 4, 0, 4 * wm, 0);
+      if (rows <= 32) MOEFP8_G2_REG(kTwoTerms, 1);
+      else if (rows <= 64) MOEFP8_G2_REG(kTwoTerms, 2);
+      else MOEFP8_G2_REG(kTwoTerms, 4);
     } else {
-      if (rows <= 32) MOEFP8_G2_UNIT(false, false, 1, 0, wm, 0);
-      else if (rows <= 64) MOEFP8_G2_UNIT(false, false, 2, 0, 2 * wm, 0);
-      else MOEFP8_G2_UNIT(false, false, 4, 0, 4 * wm, 0);
+      if (rows <= 32) MOEFP8_G2_REG(kOneTerm, 1);
+      else if (rows <= 64) MOEFP8_G2_REG(kOneTerm, 2);
+      else MOEFP8_G2_REG(kOneTerm, 4);
     }
+#undef MOEFP8_G2_REG
 #undef MOEFP8_G2_UNIT
     // next_s is written
     __syncthreads();
