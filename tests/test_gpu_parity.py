@@ -147,18 +147,22 @@ def test_full_path_reduced_shapes(T, E_local, H, I, offset):
     assert torch.all(out.cpu()[torch.from_numpy(nolocal)] == 0)
 
 
-@pytest.mark.parametrize("T,E_local,H,I", [(16, 8, 512, 256), (64, 32, 256, 256), (300, 16, 512, 256),
-                                              (1500, 32, 256, 128), (2100, 16, 512, 256)])
-def test_full_path_high_magnitude_tokens(T, E_local, H, I):
-    """Tokens with 30-120x hidden amplitude (outputs up to ~1e4) take the exact-product
-    sub-tile path; every element must still meet atol 1e-2 / rtol 2e-2."""
-    print(f"[magnitude] T={T} E_local={E_local} H={H} I={I}", flush=True)
+@pytest.mark.parametrize("T,E_local,H,I,stride", [(16, 8, 512, 256, 7), (64, 32, 256, 256, 7), (300, 16, 512, 256, 7),
+                                                     (1500, 32, 256, 128, 7), (2100, 16, 512, 256, 7),
+                                                     (2100, 16, 512, 256, 40), (2100, 16, 512, 256, 15)])
+def test_full_path_high_magnitude_tokens(T, E_local, H, I, stride):
+    """Every stride-th token with 30-120x hidden amplitude (outputs up to ~1e4) takes the
+    exact-product path; every element must still meet atol 1e-2 / rtol 2e-2.  At T = 2100 each
+    stride mixes the three layouts of exact rows: folded into the expert's last block as one or
+    two exact m-tiles, and separate exact-product blocks (stride 7: 8 folded / 18 separate, 15:
+    10 / 9, 40: 13 / 2 on these seeds)."""
+    print(f"[magnitude] T={T} E_local={E_local} H={H} I={I} stride={stride}", flush=True)
     wl = W.Workload(f"m{T}", T, 2000 + T)
     weights = W.make_weights(E_local, H, I, device="cpu", seed=5 + E_local)
     args = boosted(W.make_inputs(wl, device="cpu", E_local=E_local, H=H, I=I, weights=weights), E_local, 0)
     hss = args[3].clone()
     amp = torch.ones(T)
-    amp[::7] = torch.linspace(30.0, 120.0, len(amp[::7]))
+    amp[::stride] = torch.linspace(30.0, 120.0, len(amp[::stride]))
     hss *= amp[None, :]
     args = args[:3] + (hss,) + args[4:]
     out = moe_fp8.run(*to_dev(args))
