@@ -95,33 +95,45 @@ __device__ __forceinline__ int wave_exclusive_sum(int v) {
   return x - v;
 }
 
+constexpr int kScanLdsInts = 12288;   // 48 KB of staged counts
+
 __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a) {
   __shared__ int tot[kEGlobal * kClasses];
+  __shared__ int scan_lds[kScanLdsInts];
   __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], eb1[kEGlobal + 1];
   const int E = a.E_local, E3 = E * kClasses, nb = a.nblk, tid = threadIdx.x, lane = lane_id();
   if (tid < kUnitQueues) a.queues[tid * kQueueStride] = 0;
 
-  // canonical per-block base of each expert (relative), from the raw counts
-  for (int e = tid; e < E; e += kScanThreads) {
-    int run = 0;
-    for (int b = 0; b < nb; b++) {
-      const int* c = a.bcnt + (size_t)b * E3 + e * kClasses;
-      const int s = c[0] + c[1] + c[2];
-      a.ccnt[(size_t)b * E + e] = run;
-      run += s;
+  // Per bucket: exclusive prefix of the raw counts over blocks (relative) and the total; per
+  // expert: the same over its three buckets (the canonical per-block base).  The counts are
+  // staged through LDS a chunk of blocks at a time with all threads loading, so that the
+  // sequential prefixes read LDS instead of waiting on one global load per block.
+  static_assert(kEGlobal * kClasses <= kScanThreads && kEGlobal <= kScanThreads / 2, "scan roles");
+  const int chunk = max(1, min(nb, kScanLdsInts / E3));
+  int run_b = 0, run_e = 0;
+  for (int b0 = 0; b0 < nb; b0 += chunk) {
+    const int nbc = min(chunk, nb - b0);
+    for (int i = tid; i < nbc * E3; i += kScanThreads) scan_lds[i] = a.bcnt[(size_t)b0 * E3 + i];
+    __syncthreads();
+    if (tid < E3) {
+      for (int b = 0; b < nbc; b++) {
+        const int c = scan_lds[b * E3 + tid];
+        a.bcnt[(size_t)(b0 + b) * E3 + tid] = run_b;
+        run_b += c;
+      }
     }
-  }
-  __syncthreads();
-  // per bucket: exclusive prefix over blocks (relative) and the total
-  for (int i = tid; i < E3; i += kScanThreads) {
-    int run = 0;
-    for (int b = 0; b < nb; b++) {
-      const int c = a.bcnt[(size_t)b * E3 + i];
-      a.bcnt[(size_t)b * E3 + i] = run;
-      run += c;
+    const int e = tid - kScanThreads / 2;
+    if (e >= 0 && e < E) {
+      for (int b = 0; b < nbc; b++) {
+        const int* c = scan_lds + b * E3 + e * kClasses;
+        a.ccnt[(size_t)(b0 + b) * E + e] = run_e;
+        run_e += c[0] + c[1] + c[2];
+      }
     }
-    tot[i] = run;
+    // the chunk is read before the next one overwrites it
+    __syncthreads();
   }
+  if (tid < E3) tot[tid] = run_b;
   __syncthreads();
   // expert offsets, 16-row m-tile offsets and m-block offsets, expert by expert: blocks of rows_a
   // rows over an expert's class 0 and 1 rows (two-term C in the blocks that hold class 1 rows),
