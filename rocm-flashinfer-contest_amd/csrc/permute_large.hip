@@ -210,48 +210,29 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
   }
 }
 
-// Rank of each slot's key among the lower lanes of the wavefront holding the same key
-// (keys of one lane are distinct or -1), plus the per-key count of the wavefront.  One
-// pass per distinct key present: ballots, no LDS atomics, deterministic.
-__device__ __forceinline__ void wave_key_ranks(const int (&key)[kTopK], int (&rank)[kTopK], int* counts) {
-  uint32_t todo = 0;
+// Rank of each slot's key among the lower lanes of the wavefront holding the same key (keys of
+// one lane are distinct or -1).  Every lane ORs its bit into the LDS lane masks of its keys (the
+// wavefront's own masks; OR is order-free, so the result is deterministic), and a rank is the
+// count of lower lanes in its key's mask.  A wavefront's LDS operations complete in issue order,
+// so its reads see all of its ORs.
+__device__ __forceinline__ void wave_key_ranks(const int (&key)[kTopK], int (&rank)[kTopK],
+                                               unsigned long long* masks) {
+  const unsigned long long me = 1ull << lane_id();
 #pragma unroll
   for (int k = 0; k < kTopK; k++)
-    if (key[k] >= 0) todo |= 1u << k;
-  while (true) {
-    const uint64_t act = __ballot(todo != 0);
-    if (act == 0) break;
-    const int src = (int)__builtin_ctzll(act);
-    int mine = -1;
+    if (key[k] >= 0) atomicOr(&masks[key[k]], me);
+  __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int k = kTopK - 1; k >= 0; k--)
-      if ((todo >> k) & 1u) mine = key[k];
-    const int key0 = __builtin_amdgcn_readlane(mine, src);
-    uint64_t m = 0;
-    int slot = -1;
-#pragma unroll
-    for (int k = 0; k < kTopK; k++) {
-      const bool hit = key[k] == key0;
-      m |= __ballot(hit);
-      if (hit) slot = k;
-    }
-    const int r = lanes_below(m);
-#pragma unroll
-    for (int k = 0; k < kTopK; k++)
-      if (slot == k) {
-        rank[k] = r;
-        todo &= ~(1u << k);
-      }
-    if (lane_id() == src) counts[key0] = (int)__popcll(m);
-  }
+  for (int k = 0; k < kTopK; k++) rank[k] = key[k] >= 0 ? (int)__popcll(masks[key[k]] & (me - 1)) : 0;
 }
 
 __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a) {
-  __shared__ int wcnt[kBlkWaves][kEGlobal * kClasses];
-  __shared__ int wcan[kBlkWaves][kEGlobal];
+  // per wavefront and key, the lanes holding it: buckets (expert x class) and experts
+  __shared__ unsigned long long bmask[kBlkWaves][kEGlobal * kClasses];
+  __shared__ unsigned long long emask[kBlkWaves][kEGlobal];
   const int E = a.E_local, E3 = E * kClasses, tid = threadIdx.x, wave = tid >> 6;
-  for (int i = tid; i < kBlkWaves * kEGlobal * kClasses; i += kBlkTokens) (&wcnt[0][0])[i] = 0;
-  for (int i = tid; i < kBlkWaves * kEGlobal; i += kBlkTokens) (&wcan[0][0])[i] = 0;
+  for (int i = tid; i < kBlkWaves * E3; i += kBlkTokens) bmask[i / E3][i % E3] = 0ull;
+  for (int i = tid; i < kBlkWaves * E; i += kBlkTokens) emask[i / E][i % E] = 0ull;
   __syncthreads();
   const int t = blockIdx.x * kBlkTokens + tid;
   const bool in = t < a.T;
@@ -271,8 +252,8 @@ __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a)
       ek[k] = bk[k] >= 0 ? le : -1;
     }
   }
-  wave_key_ranks(bk, rb, wcnt[wave]);
-  wave_key_ranks(ek, re, wcan[wave]);
+  wave_key_ranks(bk, rb, bmask[wave]);
+  wave_key_ranks(ek, re, emask[wave]);
   __syncthreads();
   if (!in) return;
   int n_local = 0;
@@ -283,8 +264,8 @@ __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a)
     int pos = a.bcnt[(size_t)blockIdx.x * E3 + bk[k]] + rb[k];
     int cpos = a.ccnt[(size_t)blockIdx.x * E + ek[k]] + re[k];
     for (int w = 0; w < wave; w++) {
-      pos += wcnt[w][bk[k]];
-      cpos += wcan[w][ek[k]];
+      pos += (int)__popcll(bmask[w][bk[k]]);
+      cpos += (int)__popcll(emask[w][ek[k]]);
     }
     a.perm_token[pos] = t;
     a.perm_w[pos] = wk[k];
