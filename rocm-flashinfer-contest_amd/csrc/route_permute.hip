@@ -100,14 +100,16 @@ __device__ float token_sq_norm(const uint8_t* hidden, const float* hscale, int H
     }
 #pragma unroll
     for (int it = 0; it < 8; it++) {
+      // e4m3 -> f16 is exact, and so are the f16 squares inside the fp32 dot products
       float ss = 0.f;
 #pragma unroll
-      for (int w4 = 0; w4 < 4; w4++)
-#pragma unroll
-        for (int bb = 0; bb < 4; bb++) {
-          const float v = e4m3_to_f32(((uint32_t)q[it][w4] >> (8 * bb)) & 0xffu);
-          ss += v * v;
-        }
+      for (int w4 = 0; w4 < 4; w4++) {
+        const uint32_t word = (uint32_t)q[it][w4];
+        const v2h lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.0f, false);
+        const v2h hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.0f, true);
+        ss = __builtin_amdgcn_fdot2(lo, lo, ss, false);
+        ss = __builtin_amdgcn_fdot2(hi, hi, ss, false);
+      }
       a2 += ss * sc[it] * sc[it];
     }
   }
