@@ -19,11 +19,13 @@ namespace moefp8 {
 // Largest T served by the weight-streaming kernels.
 constexpr int64_t kDecodeMaxT = 64;
 
-// Large-T m-blocks, from the expected rows per local expert under uniform routing (T * 8 / 256
-// of them).  From T = 2048 (64 rows per expert) the class 0/1 rows of an expert go in 128-row
-// blocks for the LDS-staged GEMM1 and its exact-product rows in 32-row blocks; below, all rows
-// go in blocks of 16 * large_mt(T) rows (32 for a few dozen rows per expert, else 64).
-constexpr int64_t kBigT = 2048;
+// Large-T m-blocks.  From T = 128 the class 0/1 rows of an expert go in 128-row blocks for the
+// LDS-staged 128-row GEMMs and its exact-product rows in 32-row blocks (or folded into the last
+// class 0/1 block): even with a few rows per expert these stream each weight slice once per
+// block and took 253 / 249 / 277 / 311 µs at T = 128 / 256 / 512 / 1024 against 262 / 252 / 288
+// / 389 µs for the 4-wave kernels below.  Those (blocks of 16 * large_mt(T) rows) remain for
+// 64 < T < 128 and for shapes the 128-row kernels do not take.
+constexpr int64_t kBigT = 128;
 constexpr int kExactRows = 32;
 // (the 128-row GEMM1 addresses hidden rows with 32-bit byte offsets)
 bool large_big(int64_t T, int H, int I) {
