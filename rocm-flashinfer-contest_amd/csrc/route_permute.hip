@@ -231,18 +231,21 @@ __device__ void route_token(const float (&x)[4], const float (&b)[4], float rsf,
   }
 }
 
-// One wavefront per token (kSigmaThreads / 64 tokens per block), plus one trailing
-// block per local expert for the weight-scale estimates.
+// One leading block per local expert for the weight-scale estimates (first, so that they run
+// beside the token blocks instead of after them), then one wavefront per token
+// (kSigmaThreads / 64 tokens per block).
 __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __restrict__ logits, int logits_dt,
                                                               const void* __restrict__ bias, int bias_dt, int64_t T,
                                                               float rsf, int* __restrict__ topk_ids,
                                                               float* __restrict__ topk_w, int token_blocks,
                                                               MagArgs mg, int* __restrict__ zero, int n_zero) {
-  if ((int)blockIdx.x >= token_blocks) {
-    expert_sigma_block(mg, blockIdx.x - token_blocks);
+  const int sigma_blocks = (int)gridDim.x - token_blocks;
+  if ((int)blockIdx.x < sigma_blocks) {
+    expert_sigma_block(mg, blockIdx.x);
     return;
   }
-  for (int i = blockIdx.x * kSigmaThreads + threadIdx.x; i < n_zero; i += token_blocks * kSigmaThreads) zero[i] = 0;
+  const int tb = (int)blockIdx.x - sigma_blocks;   // token block
+  for (int i = tb * kSigmaThreads + threadIdx.x; i < n_zero; i += token_blocks * kSigmaThreads) zero[i] = 0;
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
   constexpr int kWavesPerBlock = kSigmaThreads / kWave;
@@ -250,7 +253,7 @@ __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __rest
 #pragma unroll
   for (int i = 0; i < 4; i++) b[i] = load_as_f32(bias, bias_dt, 4 * lane + i);
 
-  for (int64_t t = (int64_t)blockIdx.x * kWavesPerBlock + wave; t < T;
+  for (int64_t t = (int64_t)tb * kWavesPerBlock + wave; t < T;
        t += (int64_t)token_blocks * kWavesPerBlock) {
     float x[4];
     load_logits(logits, logits_dt, t, x);       // issued before the hidden-row loads
