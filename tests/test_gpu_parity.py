@@ -120,6 +120,10 @@ REDUCED = [
     (40, 32, 256, 128, 240),        # rank owning experts 240..271: half past the last expert
     (500, 32, 256, 128, 32),
     (300, 32, 512, 256, 240),
+    (127, 16, 512, 256, 0),         # last T of the 4-wave grouped GEMMs
+    (128, 16, 512, 256, 0),         # first T of the 128-row GEMMs
+    (129, 64, 256, 128, 192),       # 128-row GEMMs, 64 local experts, two routing groups
+    (600, 8, 768, 384, 0),          # 128-row GEMMs with 6 and 3 K-blocks
 ]
 
 
