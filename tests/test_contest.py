@@ -1,4 +1,4 @@
-"""Official-workload tooling (SURVEY-listed follow-ups): the flashinfer-trace workload reader,
+"""Official-workload tooling: the flashinfer-trace workload reader,
 the contest's matched-ratio scorer and the flashinfer-bench packaging.
 
 The scorer and reader restate the reference's call sites (flashinfer-bench itself is not
