@@ -248,15 +248,16 @@ def permute(idx, w, E_local: int, local_expert_offset: int):
 # --------------------------------------------------------------------------- expert FFN
 
 def swiglu(G1: torch.Tensor) -> torch.Tensor:
-    """``main.py:168-170``: C = silu(G1[:, I:]) * G1[:, :I] in fp32 (gate = second half)."""
+    """``main.py:168-170``: C = silu(G1[:, I:]) * G1[:, :I] in G1's dtype, fp32 as in the
+    reference (gate = second half)."""
     I = G1.shape[1] // 2
-    return torch.nn.functional.silu(G1[:, I:].float()) * G1[:, :I].float()
+    return torch.nn.functional.silu(G1[:, I:]) * G1[:, :I]
 
 
 def moe_forward(routing_logits, routing_bias, hidden_states, hidden_states_scale,
                 gemm1_weights, gemm1_weights_scale, gemm2_weights, gemm2_weights_scale,
                 local_expert_offset, routed_scaling_factor, dequant_all_upfront=False,
-                return_intermediates=False):
+                return_intermediates=False, accumulate=torch.float32):
     """fp32 restatement of ``run`` (``main.py:173-243``).
 
     Every tensor argument may be a torch tensor (any device) or an ndarray; fp8
@@ -265,6 +266,11 @@ def moe_forward(routing_logits, routing_bias, hidden_states, hidden_states_scale
     ``dequant_all_upfront`` it dequantises all local experts to fp32 before the
     loop, as the contest's torch reference does (``main.py:7-8``); the result is
     identical, only the cost differs.
+
+    ``accumulate=torch.float64`` keeps the fp32 dequantisation (``main.py:117,136``)
+    and runs GEMM1, SwiGLU, GEMM2 and the combine in fp64: an arbiter for outputs
+    whose pairs cancel (rows of ~1e4 summing to ~1e-2), where fp32 accumulation
+    order alone moves the result by ~1e-2.
     """
     def f32(x):
         if isinstance(x, torch.Tensor):
@@ -286,7 +292,7 @@ def moe_forward(routing_logits, routing_bias, hidden_states, hidden_states_scale
     s13 = torch.from_numpy(f32(gemm1_weights_scale))
     s2 = torch.from_numpy(f32(gemm2_weights_scale))
 
-    A = dequant_hidden(hidden_states, hidden_states_scale)         # [T, H] fp32
+    A = dequant_hidden(hidden_states, hidden_states_scale).to(accumulate)   # [T, H]
     idx, w, _, _ = route(logits, f32(routing_bias), routed_scaling_factor)
     dense_w = torch.from_numpy(dense_weights(idx, w, T))
 
@@ -294,7 +300,7 @@ def moe_forward(routing_logits, routing_bias, hidden_states, hidden_states_scale
         W13_all = [dequant_block(w13c[e], s13[e]) for e in range(E_local)]
         W2_all = [dequant_block(w2c[e], s2[e]) for e in range(E_local)]
 
-    out = torch.zeros((T, H), dtype=torch.float32)
+    out = torch.zeros((T, H), dtype=accumulate)
     sel = torch.from_numpy(idx.astype(np.int64))
     inter = {}
     for le in range(E_local):                                      # main.py:218
@@ -305,13 +311,13 @@ def moe_forward(routing_logits, routing_bias, hidden_states, hidden_states_scale
         if tok.numel() == 0:                                       # main.py:223
             continue
         A_e = A.index_select(0, tok)
-        W13 = W13_all[le] if dequant_all_upfront else dequant_block(w13c[le], s13[le])
+        W13 = (W13_all[le] if dequant_all_upfront else dequant_block(w13c[le], s13[le])).to(accumulate)
         G1 = A_e @ W13.t()                                         # main.py:232
         C = swiglu(G1)                                             # main.py:233
-        W2 = W2_all[le] if dequant_all_upfront else dequant_block(w2c[le], s2[le])
+        W2 = (W2_all[le] if dequant_all_upfront else dequant_block(w2c[le], s2[le])).to(accumulate)
         O = C @ W2.t()                                             # main.py:238
         w_tok = dense_w.index_select(0, tok)[:, ge]                # main.py:240
-        out.index_add_(0, tok, O * w_tok.unsqueeze(1))             # main.py:241
+        out.index_add_(0, tok, O * w_tok.to(accumulate).unsqueeze(1))   # main.py:241
         if return_intermediates:
             inter[le] = dict(tokens=tok.numpy().astype(np.int32), G1=G1, C=C, O=O)
     out_bf16 = out.to(torch.bfloat16)                              # main.py:243

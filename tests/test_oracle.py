@@ -249,6 +249,21 @@ def test_moe_forward_planted_mistake_is_caught():
     assert not torch.allclose(bad.double(), ref, rtol=2e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("name", [p.stem for p in sorted(GOLDEN.glob("moe_*.npz"))])
+def test_moe_forward_fp64_accumulation_vs_golden(name):
+    """The fp64-accumulation mode (fp32 dequantisation kept) matches the dense fp64 fixture to
+    the fp32 dequantisation's rounding, far inside the fp32 mode's distance."""
+    d = np.load(GOLDEN / f"{name}.npz")
+    out64, out_bf16 = O.moe_forward(*_golden_inputs(d), accumulate=torch.float64)
+    out32, _ = O.moe_forward(*_golden_inputs(d))
+    ref = torch.from_numpy(d["out_fp64"])
+    assert out64.dtype == torch.float64
+    err64, err32 = float((out64 - ref).abs().max()), float((out32.double() - ref).abs().max())
+    assert torch.allclose(out64, ref, rtol=1e-6, atol=5e-7), err64
+    assert 4 * err64 <= err32, (err64, err32)           # ~1.7e-7 against ~1.5e-6 on both fixtures
+    assert torch.equal(out_bf16, out64.to(torch.bfloat16))
+
+
 def test_dequant_all_upfront_is_identical():
     d = np.load(GOLDEN / "moe_t40_e6_h384_i256_off252.npz")
     a, _ = O.moe_forward(*_golden_inputs(d))
