@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOEFP8_ABI_VERSION 4
+#define MOEFP8_ABI_VERSION 5
 
 /* Operator constants (solutions/moe_fp8/main.py:22-29). */
 #define MOEFP8_E_GLOBAL 256
@@ -77,8 +77,9 @@ typedef struct moefp8_args {
   float routed_scaling_factor;       /* main.py:164, 192-193                        */
   int32_t logits_dtype;              /* moefp8_dtype                                */
   int32_t bias_dtype;                /* moefp8_dtype                                */
-  /* output (main.py:243): bf16 [T, H]; rows of tokens with no local expert are 0 */
-  uint16_t* output;
+  /* output (main.py:243): bf16 [T, H] (fp32 with output_f32); rows of tokens with no local
+   * expert are 0 */
+  void* output;
   /* optional outputs, may be NULL (used by parity tests):
    *   topk_ids        [T, 8] int32, the routed global expert ids, ascending
    *   topk_weights    [T, 8] fp32, weights[t, topk_ids[t, j]] of main.py:164
@@ -105,6 +106,11 @@ typedef struct moefp8_args {
    * expert get bf16(shared_output[t]). */
   const void* shared_output;
   int32_t shared_dtype;
+  /* 0: bf16 output, as the reference's run.  1: fp32 output, the same per-token sum before
+   * its bf16 rounding (bf16(fp32 output) equals the bf16 output bit for bit), for callers that
+   * add further partial sums and round once, such as expert-parallel ranks reducing their
+   * outputs (no counterpart in the reference, whose ranks each return bf16). */
+  int32_t output_f32;
 } moefp8_args;
 
 #define MOEFP8_NUM_STAGE_EVENTS 7

@@ -14,8 +14,8 @@ constexpr int kCombineCols = 1024;
 __global__ __launch_bounds__(256) void combine_kernel(const int* __restrict__ tok_slot,
                                                       const int* __restrict__ info,
                                                       const float* __restrict__ obuf,
-                                                      uint16_t* __restrict__ out, int H, const void* shared,
-                                                      int shared_dt) {
+                                                      void* __restrict__ out, int H, const void* shared,
+                                                      int shared_dt, int out_f32) {
   const int t = blockIdx.x;
   const int c = blockIdx.y * kCombineCols + 4 * threadIdx.x;
   const int S = info[4];
@@ -58,17 +58,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const int* __restrict__ to
     }
   }
   if (shared) add_shared4(acc, shared, shared_dt, (size_t)t * H + c);
-  uint2 o;
-  o.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
-  o.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
-  *reinterpret_cast<uint2*>(out + (size_t)t * H + c) = o;
+  store_out4(out, (size_t)t * H + c, acc, out_f32);
 }
 
 
-void launch_combine(const Plan& pl, const float* obuf, uint16_t* out, int T, int H, hipStream_t stream) {
+void launch_combine(const Plan& pl, const float* obuf, void* out, int T, int H, hipStream_t stream) {
   if (T <= 0) return;
   hipLaunchKernelGGL(combine_kernel, dim3(T, (H + kCombineCols - 1) / kCombineCols), dim3(256), 0, stream,
-                     pl.tok_slot, pl.info, obuf, out, H, pl.shared, pl.shared_dt);
+                     pl.tok_slot, pl.info, obuf, out, H, pl.shared, pl.shared_dt, pl.out_f32);
 }
 
 }  // namespace moefp8

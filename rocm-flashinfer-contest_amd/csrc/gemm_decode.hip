@@ -385,8 +385,8 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
 // a row first, summed from zero in fp32 and rounded once to bf16; tokens without a local
 // expert get zeros.  Thread = (token, 4 columns).
 __device__ void combine_columns(const int* __restrict__ tok_slot, const float* __restrict__ obuf,
-                                uint16_t* __restrict__ out, int T, int H, int S, int c0, const void* shared,
-                                int shared_dt) {
+                                void* __restrict__ out, int T, int H, int S, int c0, const void* shared,
+                                int shared_dt, int out_f32) {
   constexpr int kQuads = 16;                            // 4-column groups of the 64 columns
   const int c = c0 + 4 * (threadIdx.x % kQuads);
   for (int t = threadIdx.x / kQuads; t < T; t += blockDim.x / kQuads) {
@@ -443,17 +443,14 @@ __device__ void combine_columns(const int* __restrict__ tok_slot, const float* _
       acc.w += o.w;
     }
     if (shared) add_shared4(acc, shared, shared_dt, (size_t)t * H + c);
-    uint2 v;
-    v.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
-    v.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
-    *reinterpret_cast<uint2*>(out + (size_t)t * H + c) = v;
+    store_out4(out, (size_t)t * H + c, acc, out_f32);
   }
 }
 
 __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_decode_kernel(Problem pb, Plan pl,
                                                                                              CHalf ch,
                                                                                              float* __restrict__ obuf,
-                                                                                             uint16_t* __restrict__ out) {
+                                                                                             void* __restrict__ out) {
   __shared__ union {
     G2Stage ring[2];
     G2Pre pre;
@@ -473,10 +470,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
          i += (size_t)gridDim.x * blockDim.x) {
       float4 acc = {0.f, 0.f, 0.f, 0.f};
       if (pl.shared) add_shared4(acc, pl.shared, pl.shared_dt, 4 * i);
-      uint2 v;
-      v.x = (uint32_t)f32_to_bf16_rne(acc.x) | ((uint32_t)f32_to_bf16_rne(acc.y) << 16);
-      v.y = (uint32_t)f32_to_bf16_rne(acc.z) | ((uint32_t)f32_to_bf16_rne(acc.w) << 16);
-      reinterpret_cast<uint2*>(out)[i] = v;
+      store_out4(out, 4 * i, acc, pl.out_f32);
     }
     return;
   }
@@ -659,7 +653,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     // output columns [64 cb, 64 cb + 64) are complete once all n_mt * S units of the column
     // block stored their rows
     if (arrive_last(pl.counters2 + du.cb, n_mt * S, &last_s))
-      combine_columns(pl.tok_slot, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves, pl.shared, pl.shared_dt);
+      combine_columns(pl.tok_slot, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves, pl.shared, pl.shared_dt, pl.out_f32);
   }
 }
 
@@ -675,7 +669,7 @@ void launch_gemm1_decode(const Problem& pb, const Plan& pl, const DecodePlanArgs
                      gbuf, ch);
 }
 
-void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, uint16_t* out,
+void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, void* out,
                         hipStream_t stream) {
   if (pb.T <= 0) return;
   hipLaunchKernelGGL(gemm2_decode_kernel, dim3(decode_grid2()), dim3(64 * kDecBlockWaves), 0, stream, pb, pl, ch,

@@ -255,6 +255,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
     if (((uintptr_t)p & 3u) != 0) return MOEFP8_ERR_ALIGNMENT;
   if (!aligned_for_dtype(a->routing_logits, a->logits_dtype) || !aligned_for_dtype(a->routing_bias, a->bias_dtype))
     return MOEFP8_ERR_ALIGNMENT;
+  if (a->output_f32 != 0 && a->output_f32 != 1) return MOEFP8_ERR_DTYPE;
   if (a->shared_output) {
     if (a->shared_dtype != MOEFP8_DTYPE_F32 && a->shared_dtype != MOEFP8_DTYPE_BF16) return MOEFP8_ERR_DTYPE;
     if (!aligned16(a->shared_output)) return MOEFP8_ERR_ALIGNMENT;
@@ -285,6 +286,7 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pl.counters2 = nullptr;
   pl.shared = a->shared_output;
   pl.shared_dt = a->shared_dtype;
+  pl.out_f32 = a->output_f32;
   float* tok_a2 = reinterpret_cast<float*>(ws + L.tok_a2);
   float* esig = reinterpret_cast<float*>(ws + L.esig);
 

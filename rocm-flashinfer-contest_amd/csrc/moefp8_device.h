@@ -91,6 +91,7 @@ __device__ __forceinline__ bool needs_exact_products(float a2, float w, float s1
 }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
 // A value the caller knows to be equal on every lane, moved to a scalar register.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 // Wavefront index inside the workgroup, as a wave-uniform (scalar) value.
@@ -220,6 +221,19 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
+}
+
+// Stores output elements i .. i + 3 (i a multiple of 4): rounded to bf16 (nearest even), or
+// as fp32 when out_f32.
+__device__ __forceinline__ void store_out4(void* out, size_t i, float4 v, int out_f32) {
+  if (out_f32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(out) + i) = v;
+    return;
+  }
+  uint2 o;
+  o.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
+  o.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
+  *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + i) = o;
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }

@@ -71,6 +71,7 @@ struct Plan {
   int* counters2;             // small T: arrivals per 64 output columns, zeroed by the routing
   const void* shared;         // optional [T, H] rows added before the bf16 rounding (NULL: none)
   int shared_dt;              // 0 fp32, 1 bf16
+  int out_f32;                // output in fp32 (the sum before its bf16 rounding) instead of bf16
 };
 
 struct Problem {
@@ -95,7 +96,7 @@ int decode_grid2();
 int decode_unit_groups();
 void launch_gemm1_decode(const Problem& pb, const Plan& pl, const DecodePlanArgs& da, float* gbuf, const CHalf& ch,
                          hipStream_t stream);
-void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, uint16_t* out,
+void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, void* out,
                         hipStream_t stream);
 
 constexpr int kUnitQueues = 16;
@@ -154,7 +155,7 @@ void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, flo
 void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int max_units,
                       hipStream_t stream);
 
-void launch_combine(const Plan& pl, const float* obuf, uint16_t* out, int T, int H, hipStream_t stream);
+void launch_combine(const Plan& pl, const float* obuf, void* out, int T, int H, hipStream_t stream);
 
 // Per-token 1x128 e4m3 quantization of bf16 (x_dt 1) or fp32 (0) activations [T, H] into
 // q [T, H] and scale [H/128, T].

@@ -12,7 +12,7 @@ from pathlib import Path
 LIB_NAME = "libmoefp8.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -61,6 +61,7 @@ class MoeFp8Args(ctypes.Structure):
         ("stage_events", ctypes.c_void_p),
         ("shared_output", ctypes.c_void_p),
         ("shared_dtype", ctypes.c_int32),
+        ("output_f32", ctypes.c_int32),
     ]
 
 

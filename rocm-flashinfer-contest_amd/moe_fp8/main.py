@@ -90,7 +90,7 @@ def _scalar(x, kind):
 
 def _prepare(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
              gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
-             routed_scaling_factor, debug=None, shared_output=None):
+             routed_scaling_factor, debug=None, shared_output=None, output_dtype=torch.bfloat16):
     """Check the arguments, allocate output + workspace, fill the C argument struct."""
     lib = _abi.load()
     if not isinstance(hidden_states, torch.Tensor) or hidden_states.device.type != "cuda":
@@ -116,7 +116,9 @@ def _prepare(routing_logits, routing_bias, hidden_states, hidden_states_scale, g
     offset = _scalar(local_expert_offset, int)
     rsf = _scalar(routed_scaling_factor, float)
 
-    out = torch.empty((T, Hd), dtype=torch.bfloat16, device=device)
+    if output_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"output_dtype: expected torch.bfloat16 or torch.float32, got {output_dtype}")
+    out = torch.empty((T, Hd), dtype=output_dtype, device=device)
     ws_bytes = _abi.workspace_size(lib, T, E_local, Hd, Id)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
 
@@ -138,6 +140,7 @@ def _prepare(routing_logits, routing_bias, hidden_states, hidden_states_scale, g
     args.logits_dtype = _DT[logits.dtype]
     args.bias_dtype = _DT[bias.dtype]
     args.output = out.data_ptr()
+    args.output_f32 = 1 if output_dtype == torch.float32 else 0
     if debug is not None:
         P = T * min(TOP_K, E_local)
         debug["topk_ids"] = torch.empty((T, TOP_K), dtype=torch.int32, device=device)
@@ -165,13 +168,17 @@ def _prepare(routing_logits, routing_bias, hidden_states, hidden_states_scale, g
 
 def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
         gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
-        routed_scaling_factor, *, shared_output=None, debug=None):
+        routed_scaling_factor, *, shared_output=None, output_dtype=torch.bfloat16, debug=None):
     """Same contract as ``solutions/moe_fp8/main.py:173-243``.
 
     ``shared_output`` (optional, keyword only; no counterpart in the reference): a [T, H]
     float32 or bfloat16 device tensor, e.g. DeepSeek-V3's shared-expert output, added to each
     token's routed sum in fp32 before the single bf16 rounding (the add fused into the
     combine instead of a separate pass over the output).
+
+    ``output_dtype`` (keyword only): ``torch.bfloat16`` (the reference's) or ``torch.float32``,
+    the same per-token sum before its bf16 rounding, for callers that add further partial sums
+    (e.g. expert-parallel ranks) and round once; no counterpart in the reference.
 
     ``debug`` (optional dict) receives the device tensors ``topk_ids`` [T, 8]
     int32 (ascending global ids), ``topk_weights`` [T, 8] fp32,
@@ -180,7 +187,8 @@ def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_
     """
     lib, args, out, ws, ws_bytes, _keep = _prepare(
         routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
-        gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor, debug, shared_output)
+        gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor, debug, shared_output,
+        output_dtype)
     if args.num_tokens == 0:
         return out
     device = out.device
@@ -195,9 +203,9 @@ class Runner:
     construction and every call only crosses the C ABI (for timing loops and
     serving loops that reuse the same buffers).  Each call overwrites ``out``."""
 
-    def __init__(self, *run_args, debug=None, shared_output=None):
+    def __init__(self, *run_args, debug=None, shared_output=None, output_dtype=torch.bfloat16):
         (self.lib, self.args, self.out, self.workspace, self.ws_bytes,
-         self._keep) = _prepare(*run_args, debug=debug, shared_output=shared_output)
+         self._keep) = _prepare(*run_args, debug=debug, shared_output=shared_output, output_dtype=output_dtype)
         self.device = self.out.device
 
     def __call__(self, stage_events=None, stream=None):

@@ -104,6 +104,7 @@ def test_run_rejects_bad_arguments_before_any_launch(lib):
     assert run(_args(gemm1_weights_scale=0x100002)) == -4
     assert run(_args(shared_output=0x100000 * 12, shared_dtype=2)) == -3   # shared rows: fp32 or bf16
     assert run(_args(shared_output=0x100008, shared_dtype=1)) == -4
+    assert run(_args(output_f32=2)) == -3                                     # output: bf16 (0) or fp32 (1)
     assert run(_args(), n=1024) == -5                              # workspace too small
     assert run(_args(), w=0) == -5
     assert run(_args(num_tokens=0)) == 0                           # nothing to do, nothing launched

@@ -176,6 +176,36 @@ def test_full_path_high_magnitude_tokens(T, E_local, H, I, stride):
     assert_close(out, ref32, f"magnitude T={T}")
 
 
+@pytest.mark.parametrize("T,E_local,H,I,offset,shared", [(16, 8, 512, 256, 0, False), (64, 32, 256, 256, 32, True),
+                                                        (300, 16, 512, 256, 0, False), (2100, 16, 512, 256, 0, True),
+                                                        (0, 8, 256, 128, 0, False)])
+def test_fp32_output_is_the_sum_before_rounding(T, E_local, H, I, offset, shared):
+    """``output_dtype=torch.float32`` returns the per-token sum that the bf16 output rounds:
+    rounding it to bf16 gives the bf16 output bit for bit (small-T epilogue, combine kernel,
+    with and without shared rows, T = 0), and it meets the bar against the oracle's fp32
+    output."""
+    print(f"[fp32 out] T={T} E_local={E_local} H={H} I={I} offset={offset} shared={shared}", flush=True)
+    wl = W.Workload(f"f{T}", T, 3000 + T)
+    weights = W.make_weights(E_local, H, I, device="cpu", seed=11 + E_local)
+    args = boosted(W.make_inputs(wl, device="cpu", E_local=E_local, H=H, I=I, weights=weights,
+                                 local_expert_offset=offset), E_local, offset)
+    sh = torch.randn(T, H, generator=torch.Generator().manual_seed(T)) if shared else None
+    dargs = to_dev(args)
+    kw = {"shared_output": sh.to(DEV)} if shared else {}
+    out16 = moe_fp8.run(*dargs, **kw)
+    out32 = moe_fp8.run(*dargs, output_dtype=torch.float32, **kw)
+    torch.cuda.synchronize()
+    assert out32.dtype == torch.float32 and tuple(out32.shape) == (T, H)
+    assert torch.equal(out32.to(torch.bfloat16).view(torch.int16), out16.view(torch.int16))
+    ref32, _ = O.moe_forward(*args)
+    if shared:
+        ref32 = ref32 + sh
+    if T:
+        assert_close(out32, ref32, f"fp32 output T={T}")
+    with pytest.raises(TypeError):
+        moe_fp8.run(*dargs, output_dtype=torch.float16)
+
+
 @pytest.mark.parametrize("T,E_local,H,I,offset,case", [(8877, 8, 256, 384, 0, 11), (4852, 8, 384, 768, 64, 246)])
 def test_cancelling_outputs_against_fp64_oracle(T, E_local, H, I, offset, case):
     """Every token leans hard towards the local experts and every third token carries 30-120x
