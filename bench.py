@@ -12,7 +12,10 @@ would pay for.)  Per-step device time comes from two HIP events recorded around
 the C-ABI call.  A second pass records one event between consecutive kernels
 (the library's ``stage_events`` argument): every kernel's device time, live, on
 the stream it runs on; its sum is slightly above the per-step time because the
-extra event packets sit between the kernels.
+extra event packets sit between the kernels.  A third pass times the drop-in
+``moe_fp8.run(...)`` itself (argument checks, output and workspace allocation,
+ctypes), as a harness calls it: ``run_us_per_call`` (events just before and after
+the call) and ``run_host_us_per_call`` (host time of the call).
 
 Prints ONE JSON line.  Headline: T=16 decode (H=7168, I=2048, 32 local experts),
 in us/call; the T=8192 large-prefill line and the other synthetic workloads
@@ -59,19 +62,24 @@ class StageEvents:
 
 
 def work_counts(expert_offsets, T, H, I):
-    """Algorithmic HBM bytes and fp8 flops of one call from the routing counts."""
+    """Algorithmic HBM bytes and fp8 flops of one call from the routing counts (A active local
+    experts, P local pairs): every active expert's weights and block scales read once, every
+    token's logits, hidden row and scales read once and its bf16 output row written once.  Per
+    GEMM launch the same accounting: GEMM1 reads W13 (+ scales) of the active experts and the
+    hidden rows; GEMM2 reads W2 (+ scales).  The intermediates between the kernels (C, the
+    per-pair output rows) are not algorithmic bytes; what the kernels really move is the
+    ``traffic`` figure."""
     counts = [int(expert_offsets[i + 1] - expert_offsets[i]) for i in range(len(expert_offsets) - 1)]
     A = sum(1 for c in counts if c > 0)
     P = sum(counts)
     w13 = 2 * I * H + (2 * I // 128) * (H // 128) * 4
     w2 = H * I + (H // 128) * (I // 128) * 4
-    per_token = H + (H // 128) * 4 + 256 * 4 + H * 2
+    hidden = H + (H // 128) * 4
+    per_token = hidden + 256 * 4 + H * 2
     return dict(active_experts=A, pairs=P, bytes=A * (w13 + w2) + T * per_token + 512,
                 flops=P * (2 * H * 2 * I + 2 * I * H),
-                gemm1_bytes=A * w13 + P * (H + (H // 128) * 4) + P * I * 4,
-                gemm1_flops=P * 2 * H * 2 * I,
-                gemm2_bytes=A * w2 + P * I * 4 + P * H * 4,
-                gemm2_flops=P * 2 * I * H)
+                gemm1_bytes=A * w13 + T * hidden, gemm1_flops=P * 2 * H * 2 * I,
+                gemm2_bytes=A * w2, gemm2_flops=P * 2 * I * H)
 
 
 def measure(wl, weights, steps, warmup, flush):
@@ -127,6 +135,27 @@ def measure(wl, weights, steps, warmup, flush):
     e_b.record()
     torch.cuda.synchronize()
     warm_us = e_a.elapsed_time(e_b) * 1e3 / steps
+    # the drop-in entry point itself, as a harness calls it (checks, output + workspace allocation
+    # through the torch allocator, ctypes): device-timeline interval between events recorded just
+    # before and after each run() call, and the host time each call takes
+    import moe_fp8
+    run_args = (*act, *weights, 0, W.RSF)
+    moe_fp8.run(*run_args)
+    torch.cuda.synchronize()
+    rs = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    re_ = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    host = []
+    for i in range(steps):
+        evict()
+        torch.cuda.synchronize()
+        h0 = time.perf_counter()
+        rs[i].record()
+        moe_fp8.run(*run_args)
+        re_[i].record()
+        host.append((time.perf_counter() - h0) * 1e6)
+    torch.cuda.synchronize()
+    run_us = statistics.median(rs[i].elapsed_time(re_[i]) * 1e3 for i in range(steps))
+    run_host_us = statistics.median(host)
     T = wl.T
     H, I = W.H_FULL, W.I_FULL
     wk = work_counts(eo, T, H, I)
@@ -134,6 +163,7 @@ def measure(wl, weights, steps, warmup, flush):
     st = {s: statistics.median(v) for s, v in stages.items()}
     res = dict(workload=wl.name, T=T, us_per_call=us, us_min=min(per_step), us_max=max(per_step),
                us_mean=statistics.fmean(per_step), warm_us_per_call=warm_us, host_wall_s=wall,
+               run_us_per_call=run_us, run_host_us_per_call=run_host_us,
                stages_us=st, **wk)
     res["tflops"] = wk["flops"] / (us * 1e-6) / 1e12
     res["gbps"] = wk["bytes"] / (us * 1e-6) / 1e9
@@ -141,7 +171,8 @@ def measure(wl, weights, steps, warmup, flush):
     res["mfma_frac"] = wk["flops"] / (us * 1e-6) / FP8_PEAK
     t_roof = max(wk["bytes"] / HBM_PEAK, wk["flops"] / FP8_PEAK)
     res["roofline_frac"] = t_roof / (us * 1e-6)
-    # dominant kernel and its own roofline
+    # dominant kernel and its own roofline: bound by whichever of its algorithmic bytes at 8 TB/s
+    # or its fp8 flops at 5 PFLOP/s takes longer
     dom = max(("gemm1", "gemm2"), key=lambda s: st[s])
     k_us = st[dom]
     k_bytes, k_flops = wk[f"{dom}_bytes"], wk[f"{dom}_flops"]
@@ -152,8 +183,15 @@ def measure(wl, weights, steps, warmup, flush):
     else:
         ach = k_flops / (k_us * 1e-6) / 1e12
         roof = dict(bound="mfma", achieved=ach, peak=FP8_PEAK / 1e12, unit="TFLOP/s", frac=ach / (FP8_PEAK / 1e12))
-    roof.update(kernel=dom, kernel_us=k_us, algorithmic_bytes=k_bytes, algorithmic_flops=k_flops,
-                traffic=measured_traffic(dom, wl.name))
+    kernel = STAGE_KERNELS[(dom, "decode" if T <= 64 else "large")]
+    tr = traced_us(kernel, wl.name)
+    roof.update(kernel=kernel, kernel_us=k_us, algorithmic_bytes=k_bytes, algorithmic_flops=k_flops,
+                traffic=measured_traffic(kernel, wl.name), trace_us=tr,
+                frac_at_trace_us=(roof["frac"] * k_us / tr) if tr else None)
+    # both GEMM launches' fractions of their own bounds, from the event-bracketed stage times
+    res["gemm_fracs"] = {g: dict(us=st[g], hbm_frac=wk[f"{g}_bytes"] / (st[g] * 1e-6) / HBM_PEAK,
+                                 mfma_frac=wk[f"{g}_flops"] / (st[g] * 1e-6) / FP8_PEAK)
+                         for g in ("gemm1", "gemm2") if st[g] > 0}
     res["roofline"] = roof
     del runner
     return res
@@ -166,29 +204,35 @@ STAGE_KERNELS = {("gemm1", "decode"): "gemm1_decode_kernel", ("gemm2", "decode")
 PROFILES = ROOT / "profiles"
 
 
-def measured_traffic(stage, workload):
-    """HBM bytes per launch of the stage's kernel on this workload, from the rocprofv3 FETCH_SIZE
-    and WRITE_SIZE readings recorded in profiles/traffic_<kernel>_<workload>.txt, each divided by
+def _current_record(path, **match):
+    """A profiles/ record line, only if it was taken with the current kernel sources."""
+    from moe_fp8 import build
+    from moe_fp8.profiling import read_record
+    rec = read_record(path, **match)
+    if rec is None or rec.get("source") != build.source_hash():
+        return None
+    return rec
+
+
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch of the kernel on this workload, from the rocprofv3 FETCH_SIZE and
+    WRITE_SIZE readings recorded in profiles/traffic_<kernel>_<workload>.txt, each divided by
     what the same counter reads per byte for a plain device copy (profiles/traffic_copy.txt);
-    None when not recorded."""
-    path = "decode" if workload.startswith(("decode", "plumbing")) else "large"
-    kernel = STAGE_KERNELS.get((stage, path))
-
-    def record(name):
-        f = PROFILES / f"traffic_{name}.txt"
-        if not f.exists():
-            return None
-        for line in f.read_text().splitlines():
-            if line.startswith("record "):
-                return dict(x.split("=", 1) for x in line.split()[1:])
+    None when not recorded with the current kernel sources."""
+    from moe_fp8.profiling import copy_calibration
+    rec = _current_record(PROFILES / f"traffic_{kernel}_{workload}.txt", kernel=kernel)
+    cal = PROFILES / "traffic_copy.txt"
+    if rec is None or not cal.exists():
         return None
-
-    rec, cal = (record(f"{kernel}_{workload}") if kernel else None), record("copy")
-    if rec is None or cal is None:
-        return None
-    fetch_per_byte = float(cal["fetch_kib"]) * 1024 / float(cal["bytes"])
-    write_per_byte = float(cal["write_kib"]) * 1024 / float(cal["bytes"])
+    fetch_per_byte, write_per_byte = copy_calibration(cal)
     return round(float(rec["fetch_kib"]) * 1024 / fetch_per_byte + float(rec["write_kib"]) * 1024 / write_per_byte)
+
+
+def traced_us(kernel, workload):
+    """The kernel's mean cold-call duration in the committed rocprofv3 kernel trace of this workload
+    (profiles/moe_fp8_kernels_<workload>.md), if taken with the current kernel sources."""
+    rec = _current_record(PROFILES / f"moe_fp8_kernels_{workload}.md", kernel=kernel)
+    return float(rec["cold_us"]) if rec else None
 
 
 def copy_calibration():
@@ -319,17 +363,24 @@ def main():
         "roofline_frac": round(head["roofline_frac"], 4),
         "stages_us": {k: round(v, 2) for k, v in head["stages_us"].items()},
         "warm_us_per_call": round(head["warm_us_per_call"], 2),
+        "run_us_per_call": round(head["run_us_per_call"], 2),
+        "run_host_us_per_call": round(head["run_host_us_per_call"], 2),
+        "gemm_fracs": head["gemm_fracs"],
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
     }
     if sec is not None:
         line["t8192"] = {k: sec[k] for k in ("us_per_call", "tflops", "gbps", "hbm_frac", "mfma_frac", "roofline_frac",
-                                           "active_experts", "pairs", "stages_us", "roofline")}
+                                           "active_experts", "pairs", "stages_us", "gemm_fracs", "roofline",
+                                           "run_us_per_call", "run_host_us_per_call")}
     if quant is not None:
         line["quantize_hidden"] = quant
     if sweep:
         line["sweep"] = {k: {"us_per_call": round(v["us_per_call"], 2), "tflops": round(v["tflops"], 2),
                              "gbps": round(v["gbps"], 1), "roofline_frac": round(v["roofline_frac"], 4),
+                             "hbm_frac": round(v["hbm_frac"], 4), "mfma_frac": round(v["mfma_frac"], 4),
+                             "run_us_per_call": round(v["run_us_per_call"], 2),
+                             "run_host_us_per_call": round(v["run_host_us_per_call"], 2),
                              "P": v["pairs"], "A": v["active_experts"],
                              "stages_us": {s: round(x, 1) for s, x in v["stages_us"].items()}}
                          for k, v in sweep.items()}

@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOEFP8_ABI_VERSION 5
+#define MOEFP8_ABI_VERSION 6
 
 /* Operator constants (solutions/moe_fp8/main.py:22-29). */
 #define MOEFP8_E_GLOBAL 256
@@ -126,6 +126,15 @@ const char* moefp8_strerror(int status);
  * the torch allocator inside run()). */
 int moefp8_workspace_size(int64_t num_tokens, int32_t num_local_experts, int32_t hidden_size,
                           int32_t intermediate_size, size_t* bytes);
+
+/* Kernel family moefp8_run uses for these sizes (host only, no device needed; no counterpart in
+ * the reference, whose run() always loops over experts in Python, main.py:218-241):
+ * MOEFP8_PATH_SMALL_T (T <= 64: weight-streaming GEMMs), MOEFP8_PATH_GROUPED (4-wave grouped
+ * GEMMs) or MOEFP8_PATH_ROWS128 (128-row LDS-staged grouped GEMMs), or a negative status. */
+#define MOEFP8_PATH_SMALL_T 0
+#define MOEFP8_PATH_GROUPED 1
+#define MOEFP8_PATH_ROWS128 2
+int moefp8_path(int64_t num_tokens, int32_t num_local_experts, int32_t hidden_size, int32_t intermediate_size);
 
 /* The operator: replaces solutions/moe_fp8/main.py:173-243 (run).
  * routing (main.py:139-165) -> token permutation (main.py:216-226) ->

@@ -27,14 +27,18 @@ constexpr int64_t kDecodeMaxT = 64;
 // 64 < T < 128 and for shapes the 128-row kernels do not take.
 constexpr int64_t kBigT = 128;
 constexpr int kExactRows = 32;
-// (the 128-row GEMM1 addresses hidden rows with 32-bit byte offsets)
-bool large_big(int64_t T, int H, int I) {
+// The 128-row kernels address their DMA sources with 32-bit per-lane byte offsets from a
+// wave-uniform base: hidden rows (token x H, GEMM1) and C rows (pair x 2I, GEMM2).  Shapes whose
+// offsets could pass 2^31 (T x H) or 2^32 (Pmax x 2I, Pmax = T x min(8, E_local)) take the 4-wave
+// kernels, which form 64-bit addresses.
+bool large_big(int64_t T, int E_local, int H, int I) {
+  const int64_t pmax = T * (E_local < kTopK ? E_local : kTopK);
   return T >= kBigT && H / kBlock <= kBigMaxKB && I / kBlock <= kBigMaxKB && H % 256 == 0 &&
-         T * H < ((int64_t)1 << 31);
+         T * H < ((int64_t)1 << 31) && pmax * 2 * I < ((int64_t)1 << 32);
 }
 int large_mt(int64_t T) { return T / 32 >= 48 ? 4 : 2; }
-int large_rows_a(int64_t T, int H, int I) { return large_big(T, H, I) ? kBigRows : 16 * large_mt(T); }
-int large_rows_b(int64_t T, int H, int I) { return large_big(T, H, I) ? kExactRows : 16 * large_mt(T); }
+int large_rows_a(int64_t T, int E, int H, int I) { return large_big(T, E, H, I) ? kBigRows : 16 * large_mt(T); }
+int large_rows_b(int64_t T, int E, int H, int I) { return large_big(T, E, H, I) ? kExactRows : 16 * large_mt(T); }
 
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
@@ -93,7 +97,7 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   // large T: permutation scratch and tables, C (f16 hi, e4m3 or f16 lo, fp32 scales), O [pmax][H] fp32
   L.rows_cap = pmax;
   L.nblk = permute_large_blocks(T);
-  const int ra = large_rows_a(T, H, I), rb = large_rows_b(T, H, I);
+  const int ra = large_rows_a(T, E_local, H, I), rb = large_rows_b(T, E_local, H, I);
   // blocks per expert (both GEMMs): ceil(class 0+1 rows / ra) + ceil(class 2 rows / rb)
   const int64_t exact_blocks = (pmax + rb - 1) / rb + E_local;
   L.max_blocks = (pmax + ra - 1) / ra + E_local + exact_blocks;
@@ -201,6 +205,14 @@ int moefp8_workspace_size(int64_t num_tokens, int32_t num_local_experts, int32_t
   if (rc) return rc;
   *bytes = make_layout(num_tokens, num_local_experts, hidden_size, intermediate_size).total;
   return MOEFP8_OK;
+}
+
+int moefp8_path(int64_t num_tokens, int32_t num_local_experts, int32_t hidden_size, int32_t intermediate_size) {
+  const int rc = check_sizes(num_tokens, num_local_experts, hidden_size, intermediate_size);
+  if (rc) return rc;
+  if (num_tokens <= kDecodeMaxT) return MOEFP8_PATH_SMALL_T;
+  return large_big(num_tokens, num_local_experts, hidden_size, intermediate_size) ? MOEFP8_PATH_ROWS128
+                                                                                    : MOEFP8_PATH_GROUPED;
 }
 
 int moefp8_route(const void* routing_logits, int32_t logits_dtype, const void* routing_bias, int32_t bias_dtype,
@@ -377,9 +389,10 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   pa.mblocks = reinterpret_cast<int4*>(ws + L.mblocks);
   pa.mbgroup = reinterpret_cast<int2*>(ws + L.mbgroup);
   pa.queues = reinterpret_cast<int*>(ws + L.queues);
-  pa.mixed = large_big(T, H, I) ? 1 : 0;   // the 128-row GEMMs run mixed blocks
-  pa.rows_a = large_rows_a(T, H, I);
-  pa.rows_b = large_rows_b(T, H, I);
+  const bool big = large_big(T, E_local, H, I);
+  pa.mixed = big ? 1 : 0;   // the 128-row GEMMs run mixed blocks
+  pa.rows_a = large_rows_a(T, E_local, H, I);
+  pa.rows_b = large_rows_b(T, E_local, H, I);
   pl.canon_token = pa.canon_token;
   pl.mblocks = pa.mblocks;
   pl.mbgroup = pa.mbgroup;
@@ -396,14 +409,14 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   mark(1);
   launch_permute_large(pa, s);
   mark(2);
-  if (large_big(T, H, I)) {
+  if (big) {
     launch_gemm1_big(pb, pl, ch, (int)(L.max_blocks * (I / kBlock)), s);
   } else {
     launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks * (I / kBlock)), s);
   }
   mark(3);
   mark(4);   // SwiGLU is GEMM1's epilogue here: empty activation stage
-  if (large_big(T, H, I)) {
+  if (big) {
     launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks * (H / 256)), s);
   } else {
     launch_gemm2_large(pb, pl, ch, obuf, large_mt(T), (int)(L.max_blocks * (H / kBlock)), s);

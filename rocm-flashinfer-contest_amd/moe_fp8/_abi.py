@@ -12,7 +12,7 @@ from pathlib import Path
 LIB_NAME = "libmoefp8.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -30,8 +30,13 @@ STATUS = {
 }
 
 # Every extern "C" symbol of include/moefp8.h.
-EXPORTS = ("moefp8_abi_version", "moefp8_strerror", "moefp8_workspace_size", "moefp8_run", "moefp8_route",
-           "moefp8_quantize_hidden")
+EXPORTS = ("moefp8_abi_version", "moefp8_strerror", "moefp8_workspace_size", "moefp8_path", "moefp8_run",
+           "moefp8_route", "moefp8_quantize_hidden")
+
+# moefp8_path results
+PATH_SMALL_T = 0
+PATH_GROUPED = 1
+PATH_ROWS128 = 2
 
 
 class MoeFp8Args(ctypes.Structure):
@@ -96,6 +101,8 @@ def load(path: os.PathLike | None = None):
     lib.moefp8_workspace_size.restype = ctypes.c_int
     lib.moefp8_workspace_size.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                           ctypes.POINTER(ctypes.c_size_t)]
+    lib.moefp8_path.restype = ctypes.c_int
+    lib.moefp8_path.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
     lib.moefp8_run.restype = ctypes.c_int
     lib.moefp8_run.argtypes = [ctypes.POINTER(MoeFp8Args), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.moefp8_route.restype = ctypes.c_int

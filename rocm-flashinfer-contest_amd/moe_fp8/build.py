@@ -35,6 +35,19 @@ def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
+def source_hash() -> str:
+    """16 hex digits of SHA-256 over the kernel and ABI sources (csrc/*.hip, csrc/*.h,
+    include/moefp8.h), in name order.  Profile records carry it, so a record taken with other
+    kernels is recognised as stale."""
+    import hashlib
+    h = hashlib.sha256()
+    for f in sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + [INCLUDE / "moefp8.h"]:
+        h.update(f.name.encode())
+        h.update(b"\0")
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every HIP source for gfx950 and link ``libmoefp8.so`` (always rebuilds)."""
     cc = hipcc()

@@ -12,7 +12,10 @@ Named workloads (T tokens, 32 local experts at offset 0, H=7168, I=2048,
 routed scaling 2.5):
 
 * ``plumbing``  T=16, seed 0.
-* ``decode``    T in {1, 4, 16, 64}, seed 100+T.
+* ``decode``    T in {1, 4, 16, 64}, seed 100+T.  At T = 1 and 4 these seeds route no token to
+  local experts 0-31 (routing plus the zero output only), so
+* ``decode_t1_local`` / ``decode_t4_local`` take the first seed 100+T+k (k >= 1) whose routing
+  gives local work: seed 102 (1 pair, 1 active expert) and seed 105 (2 pairs, 2 experts).
 * ``prefill``   T=1024, seed 1024.
 * ``large``     T=8192, seed 8192; per-token hidden amplitude exp(z), z~N(0,1).
 * ``skewed``    T=5000, seed 5000; Zipf(s=1.2) expert popularity over a seeded
@@ -53,6 +56,8 @@ def workloads():
     w = {"plumbing_t16": Workload("plumbing_t16", 16, 0)}
     for T in (1, 4, 16, 64):
         w[f"decode_t{T}"] = Workload(f"decode_t{T}", T, 100 + T)
+    w["decode_t1_local"] = Workload("decode_t1_local", 1, 102)
+    w["decode_t4_local"] = Workload("decode_t4_local", 4, 105)
     w["prefill_t1024"] = Workload("prefill_t1024", 1024, 1024)
     w["large_t8192"] = Workload("large_t8192", 8192, 8192, hidden_dist="lognormal")
     w["skewed_t5000"] = Workload("skewed_t5000", 5000, 5000, routing="zipf")

@@ -130,3 +130,35 @@ def test_python_entry_point_fails_loudly_without_device_tensors(lib):
 def test_missing_library_raises(tmp_path):
     with pytest.raises(FileNotFoundError):
         _abi.load(tmp_path / "libmoefp8.so")
+
+
+def test_path_dispatch_bounds(lib):
+    """moefp8_path: T <= 64 streams weights; from T = 128 the 128-row kernels run unless their
+    32-bit DMA offsets could wrap (T x H >= 2^31, or Pmax x 2I >= 2^32 with Pmax = T x min(8,
+    E_local)), or H is not a multiple of 256, or a K range exceeds 64 blocks; those shapes take
+    the 4-wave grouped kernels (64-bit addresses)."""
+    p = lib.moefp8_path
+    H, I = 7168, 2048
+    assert p(1, 32, H, I) == _abi.PATH_SMALL_T
+    assert p(64, 32, H, I) == _abi.PATH_SMALL_T
+    assert p(65, 32, H, I) == _abi.PATH_GROUPED
+    assert p(127, 32, H, I) == _abi.PATH_GROUPED
+    assert p(128, 32, H, I) == _abi.PATH_ROWS128
+    assert p(8192, 32, H, I) == _abi.PATH_ROWS128
+    # Pmax x 2I at the 2^32 edge (E_local >= 8: Pmax = 8T)
+    assert 8 * 131071 * 2 * I < 1 << 32 <= 8 * 131072 * 2 * I
+    assert p(131071, 256, H, I) == _abi.PATH_ROWS128
+    assert p(131072, 256, H, I) == _abi.PATH_GROUPED
+    assert p(131072, 4, H, I) == _abi.PATH_ROWS128          # Pmax = 4T
+    # T x H at the 2^31 edge
+    t = (1 << 31) // H
+    assert p(t, 1, H, 128) == _abi.PATH_ROWS128
+    assert p(t + 1, 1, H, 128) == _abi.PATH_GROUPED
+    # shapes the 128-row kernels do not take
+    assert p(4096, 32, 384, I) == _abi.PATH_GROUPED         # H % 256 != 0
+    assert p(4096, 32, 128 * 65 * 2, I) == _abi.PATH_GROUPED  # H / 128 > 64
+    assert p(4096, 32, H, 128 * 65) == _abi.PATH_GROUPED    # I / 128 > 64
+    # invalid sizes
+    assert p(-1, 32, H, I) == -2
+    assert p(16, 0, H, I) == -2
+    assert p(16, 32, 100, I) == -2
