@@ -14,8 +14,9 @@ the C-ABI call.  A second pass records one event between consecutive kernels
 the stream it runs on; its sum is slightly above the per-step time because the
 extra event packets sit between the kernels.  A third pass times the drop-in
 ``moe_fp8.run(...)`` itself (argument checks, output and workspace allocation,
-ctypes), as a harness calls it: ``run_us_per_call`` (events just before and after
-the call) and ``run_host_us_per_call`` (host time of the call).
+ctypes) the way the reference's harness times a solution (flush, event, call,
+event, back to back): ``run_us_per_call``; ``run_host_us_per_call`` is the host
+time of one call.
 
 Prints ONE JSON line.  Headline: T=16 decode (H=7168, I=2048, 32 local experts),
 in us/call; the T=8192 large-prefill line and the other synthetic workloads
@@ -135,9 +136,10 @@ def measure(wl, weights, steps, warmup, flush):
     e_b.record()
     torch.cuda.synchronize()
     warm_us = e_a.elapsed_time(e_b) * 1e3 / steps
-    # the drop-in entry point itself, as a harness calls it (checks, output + workspace allocation
-    # through the torch allocator, ctypes): device-timeline interval between events recorded just
-    # before and after each run() call, and the host time each call takes
+    # the drop-in entry point itself, as the reference's harness times a solution's run()
+    # (flush, event, run(...), event, back to back without host synchronisation; its argument
+    # checks, output allocation and ctypes call overlap the flush still running on the device),
+    # and separately the host time one run() call takes
     import moe_fp8
     run_args = (*act, *weights, 0, W.RSF)
     moe_fp8.run(*run_args)
@@ -147,12 +149,11 @@ def measure(wl, weights, steps, warmup, flush):
     host = []
     for i in range(steps):
         evict()
-        torch.cuda.synchronize()
-        h0 = time.perf_counter()
         rs[i].record()
+        h0 = time.perf_counter()
         moe_fp8.run(*run_args)
-        re_[i].record()
         host.append((time.perf_counter() - h0) * 1e6)
+        re_[i].record()
     torch.cuda.synchronize()
     run_us = statistics.median(rs[i].elapsed_time(re_[i]) * 1e3 for i in range(steps))
     run_host_us = statistics.median(host)

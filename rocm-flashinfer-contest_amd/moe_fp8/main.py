@@ -45,6 +45,28 @@ TOPK_GROUP = 4
 
 _DT = {torch.float32: _abi.DTYPE_F32, torch.bfloat16: _abi.DTYPE_BF16, torch.float16: _abi.DTYPE_F16}
 
+# Workspace bytes per (T, E_local, H, I), and reusable workspaces per (device, stream) for calls
+# whose workspace is at most _WS_KEEP_MAX bytes (the small-T decode sizes of a serving loop): calls
+# on one stream run in stream order, so they can share one buffer.  Larger workspaces come from the
+# torch allocator on every call (it caches them itself) and are not held between calls.
+_WS_BYTES = {}
+_WS_KEEP = {}
+_WS_KEEP_MAX = 64 << 20
+
+
+def _workspace(lib, device, stream, T, E_local, Hd, Id):
+    key = (T, E_local, Hd, Id)
+    nbytes = _WS_BYTES.get(key)
+    if nbytes is None:
+        nbytes = _WS_BYTES[key] = _abi.workspace_size(lib, T, E_local, Hd, Id)
+    if nbytes > _WS_KEEP_MAX:
+        return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device), nbytes
+    skey = (device.index, stream)
+    ws = _WS_KEEP.get(skey)
+    if ws is None or ws.numel() < nbytes:
+        ws = _WS_KEEP[skey] = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+    return ws, nbytes
+
 
 def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else None
@@ -90,8 +112,10 @@ def _scalar(x, kind):
 
 def _prepare(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights,
              gemm1_weights_scale, gemm2_weights, gemm2_weights_scale, local_expert_offset,
-             routed_scaling_factor, debug=None, shared_output=None, output_dtype=torch.bfloat16):
-    """Check the arguments, allocate output + workspace, fill the C argument struct."""
+             routed_scaling_factor, debug=None, shared_output=None, output_dtype=torch.bfloat16,
+             reuse_workspace=False):
+    """Check the arguments, allocate output + workspace, fill the C argument struct.  With
+    ``reuse_workspace`` a small workspace is shared by the calls on the current stream."""
     lib = _abi.load()
     if not isinstance(hidden_states, torch.Tensor) or hidden_states.device.type != "cuda":
         raise ValueError("hidden_states must be a device (cuda/HIP) tensor")
@@ -119,8 +143,11 @@ def _prepare(routing_logits, routing_bias, hidden_states, hidden_states_scale, g
     if output_dtype not in (torch.bfloat16, torch.float32):
         raise TypeError(f"output_dtype: expected torch.bfloat16 or torch.float32, got {output_dtype}")
     out = torch.empty((T, Hd), dtype=output_dtype, device=device)
-    ws_bytes = _abi.workspace_size(lib, T, E_local, Hd, Id)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    if reuse_workspace and T > 0:
+        ws, ws_bytes = _workspace(lib, device, torch.cuda.current_stream(device).cuda_stream, T, E_local, Hd, Id)
+    else:
+        ws_bytes = _abi.workspace_size(lib, T, E_local, Hd, Id)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
 
     args = _abi.MoeFp8Args()
     args.routing_logits = logits.data_ptr()
@@ -188,13 +215,17 @@ def run(routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_
     lib, args, out, ws, ws_bytes, _keep = _prepare(
         routing_logits, routing_bias, hidden_states, hidden_states_scale, gemm1_weights, gemm1_weights_scale,
         gemm2_weights, gemm2_weights_scale, local_expert_offset, routed_scaling_factor, debug, shared_output,
-        output_dtype)
+        output_dtype, reuse_workspace=True)
     if args.num_tokens == 0:
         return out
     device = out.device
-    stream = torch.cuda.current_stream(device).cuda_stream
-    with torch.cuda.device(device):
+    if torch.cuda.current_device() == device.index:
+        stream = torch.cuda.current_stream(device).cuda_stream
         _abi.check(lib, lib.moefp8_run(ctypes.byref(args), ws.data_ptr(), ws_bytes, stream))
+    else:
+        with torch.cuda.device(device):
+            stream = torch.cuda.current_stream(device).cuda_stream
+            _abi.check(lib, lib.moefp8_run(ctypes.byref(args), ws.data_ptr(), ws_bytes, stream))
     return out
 
 
