@@ -49,7 +49,8 @@ typedef enum moefp8_status {
   MOEFP8_ERR_ALIGNMENT = -4,      /* a pointer is not 16-byte aligned */
   MOEFP8_ERR_WORKSPACE = -5,      /* workspace NULL or smaller than moefp8_workspace_size() */
   MOEFP8_ERR_LAUNCH = -6,         /* a kernel launch failed (hipGetLastError) */
-  MOEFP8_ERR_DEVICE = -7          /* current device is not gfx950 / HIP runtime error */
+  MOEFP8_ERR_DEVICE = -7,         /* current device is not gfx950 / HIP runtime error */
+  MOEFP8_ERR_SCRATCH_LIMIT = -8   /* moefp8_run_noalloc: the sizes need more than its static scratch */
 } moefp8_status;
 
 /* dtype codes for routing_logits / routing_bias (main.py:145-146 upcast both to fp32). */
@@ -142,6 +143,20 @@ int moefp8_path(int64_t num_tokens, int32_t num_local_experts, int32_t hidden_si
  * weighted combine + bf16 round (main.py:240-243), all enqueued on `stream`
  * (a hipStream_t; NULL = legacy default stream). */
 int moefp8_run(const moefp8_args* args, void* workspace, size_t workspace_bytes, void* stream);
+
+/* The operator without allocation.  No counterpart in the reference (whose run() allocates
+ * through the torch allocator, main.py:202, 226-241): for callers that cannot allocate device
+ * memory, such as code under HIP graph capture, tight serving loops and harnesses that forbid
+ * hipMalloc.  Same arguments, work and results as moefp8_run, but the workspace is a static
+ * device array of MOEFP8_NOALLOC_SCRATCH_BYTES (64 MiB) per device that loads the library, held
+ * until the process ends; sizes whose moefp8_workspace_size() exceeds it return
+ * MOEFP8_ERR_SCRATCH_LIMIT before any launch (it covers every T <= 64 of the operator's shapes,
+ * H = 7168, I = 2048, any E_local, and T up to ~160 on the grouped path).  The call itself
+ * allocates nothing.  Every call on a device shares that device's array: calls that overlap on
+ * one device (different streams, or other host threads) race and must be serialised by the
+ * caller; calls on one stream are ordered by it.  Each call initialises what it reads. */
+#define MOEFP8_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int moefp8_run_noalloc(const moefp8_args* args, void* stream);
 
 /* Routing alone: replaces solutions/moe_fp8/main.py:139-165 (_route).
  * Writes topk_ids [T, 8] int32 (ascending ids) and topk_weights [T, 8] fp32. */

@@ -116,6 +116,24 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   return L;
 }
 
+// Device memory of the no-allocation entry point: one static array per device that loads the
+// library, held until the process ends.  Host code never uses the name `scratch` as an address
+// (on the host it is a stand-in, not device memory): the device address comes from
+// hipGetSymbolAddress, once per device, and is kept in g_scratch_ptr.
+constexpr size_t kScratchBytes = MOEFP8_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+static std::atomic<void*> g_scratch_ptr[64];
+
+// This device's address of `scratch` (the device must be current); NULL if the runtime cannot
+// give it.
+static void* scratch_address(int dev) {
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+  g_scratch_ptr[dev].store(p, std::memory_order_release);   // same value if two threads race here
+  return p;
+}
+
 static std::atomic<int> g_cu_count[64];
 static std::atomic<int> g_arch_ok[64];  // 0 unknown, 1 gfx950, -1 other
 
@@ -194,6 +212,9 @@ const char* moefp8_strerror(int status) {
     case MOEFP8_ERR_WORKSPACE: return "workspace is NULL or smaller than moefp8_workspace_size()";
     case MOEFP8_ERR_LAUNCH: return "kernel launch failed";
     case MOEFP8_ERR_DEVICE: return "current HIP device is not gfx950 or the HIP runtime failed";
+    case MOEFP8_ERR_SCRATCH_LIMIT:
+      return "sizes need more workspace than moefp8_run_noalloc's static scratch (MOEFP8_NOALLOC_SCRATCH_BYTES, "
+             "64 MiB)";
     default: return "unknown status";
   }
 }
@@ -248,7 +269,9 @@ int moefp8_quantize_hidden(const void* x, int32_t x_dtype, int64_t num_tokens, i
   return hipGetLastError() == hipSuccess ? MOEFP8_OK : MOEFP8_ERR_LAUNCH;
 }
 
-int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+// The operator on the caller's workspace, or with `noalloc` on this device's static scratch, for
+// sizes whose workspace fits it (moefp8_run_noalloc).
+static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_bytes, void* stream, bool noalloc) {
   if (!a) return MOEFP8_ERR_NULL_POINTER;
   const int64_t T = a->num_tokens;
   const int E_local = a->num_local_experts, H = a->hidden_size, I = a->intermediate_size;
@@ -273,9 +296,14 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
     if (!aligned16(a->shared_output)) return MOEFP8_ERR_ALIGNMENT;
   }
   const Layout L = make_layout(T, E_local, H, I);
-  if (!workspace || workspace_bytes < L.total || !aligned16(workspace)) return MOEFP8_ERR_WORKSPACE;
+  if (noalloc) {
+    if (L.total > kScratchBytes) return MOEFP8_ERR_SCRATCH_LIMIT;
+  } else if (!workspace || workspace_bytes < L.total || !aligned16(workspace)) {
+    return MOEFP8_ERR_WORKSPACE;
+  }
   int dev;
   if (query_device(&dev)) return MOEFP8_ERR_DEVICE;
+  if (noalloc && !(workspace = scratch_address(dev))) return MOEFP8_ERR_DEVICE;
 
   hipStream_t s = (hipStream_t)stream;
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
@@ -426,5 +454,11 @@ int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, vo
   mark(6);
   return finish(a, L, topk_ids, topk_w, pl, s);
 }
+
+int moefp8_run(const moefp8_args* a, void* workspace, size_t workspace_bytes, void* stream) {
+  return run_impl(a, workspace, workspace_bytes, stream, false);
+}
+
+int moefp8_run_noalloc(const moefp8_args* a, void* stream) { return run_impl(a, nullptr, 0, stream, true); }
 
 }  // extern "C"

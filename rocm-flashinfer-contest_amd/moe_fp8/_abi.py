@@ -27,11 +27,15 @@ STATUS = {
     -5: "MOEFP8_ERR_WORKSPACE",
     -6: "MOEFP8_ERR_LAUNCH",
     -7: "MOEFP8_ERR_DEVICE",
+    -8: "MOEFP8_ERR_SCRATCH_LIMIT",
 }
 
 # Every extern "C" symbol of include/moefp8.h.
 EXPORTS = ("moefp8_abi_version", "moefp8_strerror", "moefp8_workspace_size", "moefp8_path", "moefp8_run",
-           "moefp8_route", "moefp8_quantize_hidden")
+           "moefp8_run_noalloc", "moefp8_route", "moefp8_quantize_hidden")
+
+# MOEFP8_NOALLOC_SCRATCH_BYTES: static scratch of moefp8_run_noalloc
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # moefp8_path results
 PATH_SMALL_T = 0
@@ -105,6 +109,8 @@ def load(path: os.PathLike | None = None):
     lib.moefp8_path.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
     lib.moefp8_run.restype = ctypes.c_int
     lib.moefp8_run.argtypes = [ctypes.POINTER(MoeFp8Args), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.moefp8_run_noalloc.restype = ctypes.c_int
+    lib.moefp8_run_noalloc.argtypes = [ctypes.POINTER(MoeFp8Args), ctypes.c_void_p]
     lib.moefp8_route.restype = ctypes.c_int
     lib.moefp8_route.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64,
                                  ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]

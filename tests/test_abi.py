@@ -162,3 +162,21 @@ def test_path_dispatch_bounds(lib):
     assert p(-1, 32, H, I) == -2
     assert p(16, 0, H, I) == -2
     assert p(16, 32, 100, I) == -2
+
+
+def test_noalloc_entry_point_limits_before_any_launch(lib):
+    """moefp8_run_noalloc validates like moefp8_run and rejects sizes whose workspace exceeds its
+    64 MiB static scratch with MOEFP8_ERR_SCRATCH_LIMIT, before touching the device."""
+    f = lambda a: lib.moefp8_run_noalloc(ctypes.byref(a), None)
+    assert lib.moefp8_run_noalloc(None, None) == -1
+    assert f(_args(hidden_size=100)) == -2
+    assert f(_args(routing_logits=None)) == -1
+    assert f(_args(hidden_states=0x100001)) == -4
+    assert f(_args(num_tokens=0)) == 0
+    assert f(_args(num_tokens=8192)) == -8
+    assert f(_args(num_tokens=1024)) == -8
+    assert lib.moefp8_strerror(-8).startswith(b"sizes need more workspace")
+    # every small-T shape of the operator fits the scratch
+    for T in (1, 4, 16, 64):
+        for E in (1, 32, 256):
+            assert _abi.workspace_size(lib, T, E, 7168, 2048) <= _abi.NOALLOC_SCRATCH_BYTES
