@@ -114,7 +114,7 @@ __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, Dec
   __syncthreads();
 
   // pair rows: rank of the token inside its expert (popcount of the lower tokens); the
-  // m-tile flags are the OR of its pairs' precision flags
+  // m-tile flags are the OR of its pairs' predicted precision flags
   for (int i0 = 0; i0 < NP; i0 += nth) {
     const int i = i0 + tid;
     const int t = i >> 3, j = i & 7;

@@ -125,9 +125,11 @@ __device__ __forceinline__ bool arrive_last(int* counter, int expected, int* fla
 
 // SwiGLU of pair p's C columns [128 cb, 128 cb + 128) by one wavefront: sums the GEMM1
 // partials of the S K-splits in split order, applies silu(gate) * up and writes C as two
-// f16 terms with one scale (max |C| -> 448).
+// f16 terms with one scale (max |C| -> 448).  The block's max |C| against the pair's routing
+// weight w and its expert's W2 scale sigma2 decides whether GEMM2 needs both terms in this m-tile
+// (needs_two_terms): *two_term is then set.
 __device__ __forceinline__ void swiglu_block(int I, int S, int p, int cb, const float* __restrict__ gbuf,
-                                             const CHalf& ch) {
+                                             const CHalf& ch, float w, float sigma2, int* two_term) {
   constexpr int kBatch = 8;   // partial loads issued together
   const int CB = I / kBlock, I2 = 2 * I;
   const int lane = lane_id();
@@ -154,6 +156,7 @@ __device__ __forceinline__ void swiglu_block(int I, int S, int p, int cb, const 
   }
   const float c0 = silu_f32(gate.x) * up.x, c1 = silu_f32(gate.y) * up.y;
   const float amax = wave_max_f32(fmaxf(fabsf(c0), fabsf(c1)));
+  if (lane == 0 && needs_two_terms(w, sigma2, amax, sqrtf((float)I))) atomicOr(two_term, 1);
   float inv, scale;
   split_scale(amax, inv, scale);
   _Float16 h0, l0, h1, l1;
@@ -375,8 +378,19 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
     // blocks 2j, 2j + 1 ("up") and NCB/2 + 2j, NCB/2 + 2j + 1 ("gate"), S K-splits each.
     // Every unit publishes its partials and counts itself in; the last one forms C.
     const int j = (du.cb % (NCB / 2)) / 2;
-    if (arrive_last(pl.counters + du.g * (I / kBlock) + j, 4 * S, &last_s))
-      for (int r = wave; r < M; r += kDecBlockWaves) swiglu_block(I, S, row0 + r, j, gbuf, ch);
+    if (arrive_last(pl.counters + du.g * (I / kBlock) + j, 4 * S, &last_s)) {
+      const float sigma2 = da.esig[2 * e + 1];
+      for (int r = wave; r < M; r += kDecBlockWaves) {
+        // the pair's routing weight: its token's slot holding this expert (the routing outputs
+        // are complete before this launch)
+        const int t = plan.tok[row0 + r];
+        float w = 0.f;
+#pragma unroll
+        for (int k = 0; k < kTopK; k++)
+          if (da.topk_ids[t * kTopK + k] - da.offset == e) w = da.topk_w[t * kTopK + k];
+        swiglu_block(I, S, row0 + r, j, gbuf, ch, w, sigma2, pl.two_term + du.g);
+      }
+    }
   }
 }
 
@@ -482,7 +496,9 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     const int lr = lane & 15, kg = lane >> 4;
     const DecUnit du = decode_unit(u, S, NCB);
     const int4 mt = pl.mtiles[du.g];
-    const int e = uniform(mt.x), row0 = uniform(mt.y), M = uniform(mt.z), flags = uniform(mt.w);
+    const int e = uniform(mt.x), row0 = uniform(mt.y), M = uniform(mt.z);
+    // both f16 terms of C: predicted (the plan), or measured by GEMM1
+    const bool two = (uniform(mt.w) & kFlagTwoTermC) || uniform(pl.two_term[du.g]) != 0;
     const int kb0 = du.s * KB / S, n = (du.s + 1) * KB / S - kb0;
     const int cg = du.cb * kDecBlockWaves + wave;
     const uint8_t* bp = pb.w2 + ((size_t)e * H + cg * 16 + lr) * I + (size_t)kb0 * kBlock + kg * 32;
@@ -490,7 +506,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     const int prow = row0 + (lr < M ? lr : 0);
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 
-    if (!(flags & kFlagTwoTermC) && M <= kPreRows && n <= kPre2MaxKB) {
+    if (!two && M <= kPreRows && n <= kPre2MaxKB) {
       const float swv = swp[min(lane, n - 1)];
       // weights as whole lines, transposed per wavefront through LDS (as in GEMM1)
       const int wr = lane >> 3, wc = lane & 7;
@@ -565,7 +581,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       for (int d = 0; d < kDecDepth - 1; d++)
         if (j + d < n) step(d, j + d);
       __syncthreads();
-    } else if (!(flags & kFlagTwoTermC)) {
+    } else if (!two) {
       constexpr int kStepDepth2 = 2;   // (register budget shared with the staged path)
       // carriers: wave q loads rows 4q .. 4q + 3 of C's hi term as whole lines (lane l: row
       // 4q + l/16, 16-byte chunk l%16) and publishes them chunk-major; wave 0's lanes < 16 the

@@ -15,17 +15,16 @@
 //
 // Block scales are applied per 128-K block in fp32: acc += MFMA(A_kb, B_kb) * sa[row] * sw.
 //
-// GEMM1  G1 = A_e W13_e^T on the e4m3 MFMA (m-blocks holding a pair flagged for exact
+// GEMM1  G1 = A_e W13_e^T on the e4m3 MFMA (m-blocks holding a pair predicted to need exact
 //        products: f16 MFMA on widened operands), SwiGLU in the epilogue (main.py:229-233),
-//        and C written as hi = f16(C/s), s = max|C row block| / 448 per 128 cols, plus a lo
-//        term: e4m3(2^11 (C/s - hi)) (about 15 significant bits in all), or f16(C/s - hi)
-//        (22 bits) in m-blocks with exact-product pairs, whose outputs reach 1e4 and may
-//        cancel in the per-token sum.
+//        and C written as hi = f16(C/s), s = max|C row block| / 448 per 128 cols, and
+//        lo = f16(C/s - hi) (22 significant bits together).
+// flags  per m-block, whether GEMM2 needs both terms of C (needs_two_terms on each row's max |C|
+//        per 128 columns, from the scales GEMM1 wrote).
 // GEMM2  O = C W2_e^T (main.py:234-238): C's hi term on the f16 MFMA against W2 widened
-//        to f16 (exact products, 2^-11 relative input error); m-blocks holding a pair that
-//        needs more add the e4m3 lo term on the scaled e4m3 MFMA (2^-11), or the f16 lo term
-//        on the f16 MFMA.  Rows are scaled by the routing weight (main.py:240) and summed per
-//        token by the combine kernel.
+//        to f16 (exact products, 2^-11 relative input error); m-blocks flagged by GEMM1 add
+//        the lo term on the f16 MFMA.  Rows are scaled by the routing weight (main.py:240)
+//        and summed per token by the combine kernel.
 #include "moefp8_device.h"
 #include "moefp8_launch.h"
 
@@ -35,7 +34,6 @@ constexpr int kLgWaves = 4;
 constexpr int kLgThreads = 64 * kLgWaves;
 constexpr int kLgDepth = 2;                  // weight K-blocks in flight per wavefront
 constexpr int kLgStages = kLgDepth + 1;      // activation stages in LDS
-constexpr float kLoScale = 2048.0f;          // lo term of C is stored x 2^11
 
 template <int kCount>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -138,10 +136,12 @@ __device__ __forceinline__ v8i cat(v4i x, v4i y) { return __builtin_shufflevecto
 
 __device__ __forceinline__ v8h as_v8h(v4i x) { return __builtin_bit_cast(v8h, x); }
 
-// e4m3 MFMA with A scaled by 2^(e - 127) exactly.
-template <int kExp>
-__device__ __forceinline__ v4f mfma16x16x128_exp(const v8i& a, const v8i& b, const v4f& c) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, kExp, 0, 127);
+// Writes C's two f16 terms of one element at p * I + col.
+__device__ __forceinline__ void store_c(const CHalf8& ch, size_t p, int I, int col, float c, float inv) {
+  const float v = fminf(fmaxf(c * inv, -448.0f), 448.0f);
+  const _Float16 hi = (_Float16)v;
+  ch.hi[p * I + col] = hi;
+  ch.lo16[p * I + col] = (_Float16)(v - (float)hi);
 }
 
 // ------------------------------------------------------------------------------------------ units
@@ -329,13 +329,11 @@ __device__ __forceinline__ void gemm1_large_pass(const Problem& pb, const Plan& 
   wait_vmcnt<0>();
 }
 
-// Epilogue of m-tiles [i0, i0 + NA): C = silu(gate) * up and its split.  amax_s holds, per
-// wavefront and row, the largest |C| of the wavefront's 32 columns.  kLo16 (m-blocks with
-// exact-product pairs): the lo term is f16(C/s - hi), 22 significant bits in all, instead of
-// the e4m3 2^11 (C/s - hi).
-template <int MT, int NA, bool kLo16>
-__device__ __forceinline__ void gemm1_large_store(const Plan& pl, const CHalf8& ch, float (*amax_s)[16 * MT], int I,
-                                                  int row0, int rows, int cb, int i0, const v4f (&acc)[NA][4]) {
+// Epilogue of m-tiles [i0, i0 + NA): C = silu(gate) * up and its split into two f16 terms.
+// amax_s holds, per wavefront and row, the largest |C| of the wavefront's 32 columns.
+template <int MT, int NA>
+__device__ __forceinline__ void gemm1_large_store(const CHalf8& ch, float (*amax_s)[16 * MT], int I, int row0,
+                                                  int rows, int cb, int i0, const v4f (&acc)[NA][4]) {
   const int NCB = I / kBlock;
   const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
   const int col0 = cb * kBlock + 32 * wave;
@@ -370,14 +368,7 @@ __device__ __forceinline__ void gemm1_large_store(const Plan& pl, const CHalf8& 
       split_scale(amax, inv, scale);
       const size_t p = (size_t)(row0 + row);
 #pragma unroll
-      for (int jn = 0; jn < 2; jn++) {
-        const int col = col0 + 16 * jn + lr;
-        const float v = fminf(fmaxf(c[ia][jn][r] * inv, -448.0f), 448.0f);
-        const _Float16 hi = (_Float16)v;
-        ch.hi[p * I + col] = hi;
-        if constexpr (kLo16) ch.lo16[p * I + col] = (_Float16)(v - (float)hi);
-        else ch.lo[p * I + col] = (uint8_t)f32_to_e4m3(fminf(fmaxf((v - (float)hi) * kLoScale, -448.0f), 448.0f));
-      }
+      for (int jn = 0; jn < 2; jn++) store_c(ch, p, I, col0 + 16 * jn + lr, c[ia][jn][r], inv);
       if (wave == 0 && lr == 0) ch.scale[p * NCB + cb] = scale;
     }
   }
@@ -404,14 +395,14 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, 
     if (!(flags & kFlagExactProducts)) {
       v4f acc[MT][4];
       gemm1_large_pass<MT, MT, false>(pb, pl, ring, e, row0, rows, cb, 0, acc);
-      gemm1_large_store<MT, MT, false>(pl, ch, amax_s, I, row0, rows, cb, 0, acc);
+      gemm1_large_store<MT, MT>(ch, amax_s, I, row0, rows, cb, 0, acc);
     } else {
       // two m-tiles per pass over K, with exact products (the f16 MFMA on widened operands
       // needs the registers of the fp8 path twice over)
       for (int i0 = 0; i0 < mvalid; i0 += 2) {
         v4f acc[2][4];
         gemm1_large_pass<MT, 2, true>(pb, pl, ring, e, row0, rows, cb, i0, acc);
-        gemm1_large_store<MT, 2, true>(pl, ch, amax_s, I, row0, rows, cb, i0, acc);
+        gemm1_large_store<MT, 2>(ch, amax_s, I, row0, rows, cb, i0, acc);
       }
     }
   }
@@ -492,8 +483,7 @@ __device__ __forceinline__ TileSplit mixed_split(const RowMap& rm, int wm) {
 template <int NT, bool kExact>
 __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float2* sw_s, float (*amax_s)[kBgRows],
-                                               int e, int row0, int rows, int cb, int flags, int* next_s,
-                                               int n_units) {
+                                               int e, int row0, int rows, int cb, int* next_s, int n_units) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
   static_assert(!kExact || NT == 1, "exact-product blocks hold at most 32 rows");
   const int H = pb.H, I = pb.I, T = pb.T, KB = H / kBlock, NCB = I / kBlock;
@@ -617,7 +607,6 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
     }
   }
   __syncthreads();
-  const bool two = (flags & kFlagTwoTermC) != 0;
 #pragma unroll
   for (int i = 0; i < NT; i++) {
     const int t = NT * wm + i;
@@ -630,15 +619,7 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
       split_scale(amax, inv, scale);
       const size_t p = (size_t)(row0 + row);
 #pragma unroll
-      for (int jn = 0; jn < 2; jn++) {
-        const int col = col0 + 16 * jn + lr;
-        const float v = fminf(fmaxf(c[i][jn][r] * inv, -448.0f), 448.0f);
-        const _Float16 hi = (_Float16)v;
-        ch.hi[p * I + col] = hi;
-        if constexpr (kExact) ch.lo16[p * I + col] = (_Float16)(v - (float)hi);
-        else if (two)   // GEMM2 reads it in blocks holding class 1 rows
-          ch.lo[p * I + col] = (uint8_t)f32_to_e4m3(fminf(fmaxf((v - (float)hi) * kLoScale, -448.0f), 448.0f));
-      }
+      for (int jn = 0; jn < 2; jn++) store_c(ch, p, I, col0 + 16 * jn + lr, c[i][jn][r], inv);
       if (wn == 0 && lr == 0) ch.scale[p * NCB + cb] = scale;
     }
   }
@@ -652,8 +633,8 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
 template <int NF, int NX>
 __device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float2* sw_s, float (*amax_s)[kBgRows],
-                                               int e, const RowMap& rm, int cb, bool two, int tf0, int tx0,
-                                               int* next_s, int n_units) {
+                                               int e, const RowMap& rm, int cb, int tf0, int tx0, int* next_s,
+                                               int n_units) {
   constexpr int NT = NF + NX;
   static_assert(NT >= 1 && NT <= 4, "m-tiles per wavefront");
   const int H = pb.H, I = pb.I, T = pb.T, KB = H / kBlock, NCB = I / kBlock;
@@ -789,17 +770,8 @@ __device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Pl
       float inv, scale;
       split_scale(amax, inv, scale);
       const size_t p = (size_t)rm.src(R);
-      const bool exact_row = R >= rm.xfrom;
 #pragma unroll
-      for (int jn = 0; jn < 2; jn++) {
-        const int col = col0 + 16 * jn + lr;
-        const float v = fminf(fmaxf(c[i][jn][r] * inv, -448.0f), 448.0f);
-        const _Float16 hi = (_Float16)v;
-        ch.hi[p * I + col] = hi;
-        if (exact_row) ch.lo16[p * I + col] = (_Float16)(v - (float)hi);
-        else if (two)   // GEMM2 reads it in blocks holding class 1 rows
-          ch.lo[p * I + col] = (uint8_t)f32_to_e4m3(fminf(fmaxf((v - (float)hi) * kLoScale, -448.0f), 448.0f));
-      }
+      for (int jn = 0; jn < 2; jn++) store_c(ch, p, I, col0 + 16 * jn + lr, c[i][jn][r], inv);
       if (wn == 0 && lr == 0) ch.scale[p * NCB + cb] = scale;
     }
   }
@@ -807,7 +779,10 @@ __device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Pl
 
 // Units (m-block, 128 C columns) over the blocks (128-row class 0/1 blocks, mixed blocks and
 // 32-row exact-product blocks).
-__global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Plan pl, CHalf8 ch) {
+// One workgroup per CU (its LDS ring), i.e. two wavefronts per SIMD: stated, so that the compiler
+// schedules the K loop for that occupancy instead of squeezing registers for three.
+__global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm1_big_kernel(
+    Problem pb, Plan pl, CHalf8 ch) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kBgStages * kBgStage];
   __shared__ __attribute__((aligned(16))) float2 sw_s[kBigMaxKB];
   __shared__ float amax_s[4][kBgRows];
@@ -834,10 +809,9 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Pl
     }
     __syncthreads();
     const RowMap rm = row_map(row0, rows, flags);
-    const bool two = (flags & kFlagTwoTermC) != 0;
     const int wm = wave_index() & 1;
 #define MOEFP8_G1_UNIT(NF, NX, TF0, TX0) \
-  gemm1_big_mixed_unit<NF, NX>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, rm, cb, two, TF0, TX0, &next_s, n_units)
+  gemm1_big_mixed_unit<NF, NX>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, rm, cb, TF0, TX0, &next_s, n_units)
     if (flags & kFlagMixed) {
       const TileSplit ts = mixed_split(rm, wm);
       const int nf = uniform(ts.nf), tf0 = uniform(ts.tf0), tx0 = uniform(ts.tx0);
@@ -854,7 +828,7 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Pl
       }
     } else {
 #define MOEFP8_G1_REG(NT, EXACT) \
-  gemm1_big_unit<NT, EXACT>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, flags, &next_s, n_units)
+  gemm1_big_unit<NT, EXACT>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, &next_s, n_units)
       if (flags & kFlagExactProducts) MOEFP8_G1_REG(1, true);
       else if (rows <= 32) MOEFP8_G1_REG(1, false);
       else if (rows <= 64) MOEFP8_G1_REG(2, false);
@@ -868,19 +842,17 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm1_big_kernel(Problem pb, Pl
 }
 
 // ------------------------------------------------------------------------------------------ GEMM2
-// Modes of an m-block, from the flags of its m-tiles: one term (C's hi only), two terms (hi and
-// the e4m3 lo term, MT m-tiles per pass), precise (hi and the f16 lo term, MT/2 m-tiles per
-// pass so that both f16 planes fit the same stage).
-constexpr int kOneTerm = 0, kTwoTerms = 1, kPrecise = 2;
+// Modes of an m-block: one term (C's hi only, MT m-tiles per pass), or two terms (hi and the f16
+// lo term, for blocks GEMM1 flagged; MT/2 m-tiles per pass so that both planes fit the stage).
+constexpr int kOneTerm = 0, kTwoTerms = 1;
 
-// LDS stage: [hi: MT x 4096 B][lo: MT x 2048 B][4 x 64 row scales].  An m-tile's hi (and f16
-// lo) term is [16 chunks of 16 B][16 rows][16 B]; its e4m3 lo term is [8 chunks][16 rows][16 B].
-// The precise mode puts its NP = MT/2 m-tiles of hi at 0 and of f16 lo at NP x 4096.
+// LDS stage: [hi: MT x 4096 B][4 x 64 row scales].  An m-tile's hi (and lo) term is [16 chunks of
+// 16 B][16 rows][16 B].  The two-term mode puts its NP = MT/2 m-tiles of hi at 0 and of lo at
+// NP x 4096.
 template <int MT>
 struct G2L {
   static constexpr int kHi = MT * 4096;
-  static constexpr int kLo = MT * 2048;
-  static constexpr int kScales = kHi + kLo;
+  static constexpr int kScales = kHi;
   static constexpr int kStage = kScales + kLgWaves * 64 * 4;
 };
 
@@ -888,7 +860,7 @@ struct G2L {
 // lo DMAs, the row-scale DMA and 2 weight tiles x 2 loads.
 template <int NP, int kMode>
 constexpr int g2_ops() {
-  return NP + (kMode == kTwoTerms ? NP / 2 : kMode == kPrecise ? NP : 0) + 1 + 4;
+  return NP + (kMode == kTwoTerms ? NP : 0) + 1 + 4;
 }
 
 // One pass over K for m-tiles [i0, i0 + NP) of the unit's m-block.  As in GEMM1, every m-tile
@@ -898,14 +870,12 @@ template <int MT, int NP, int kMode>
 __device__ __forceinline__ void gemm2_large_pass(const Problem& pb, const CHalf8& ch, uint8_t* ring, int e, int row0,
                                                  int rows, int hb, int i0, v4f (&acc)[NP][2]) {
   using L = G2L<MT>;
-  static_assert(kMode != kTwoTerms || NP % 2 == 0, "e4m3 lo DMA carries two m-tiles per wavefront pair");
-  constexpr int kLoDma = kMode == kTwoTerms ? NP / 2 : kMode == kPrecise ? NP : 0;
+  constexpr int kLoDma = kMode == kTwoTerms ? NP : 0;
   const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock;
   const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
   const uint8_t* bp = pb.w2 + ((size_t)e * H + hb * kBlock + 32 * wave + lr) * I + kg * 32;
   const float* swp = pb.s2 + ((size_t)e * HB + hb) * KB;
-  // hi (and f16 lo) DMA: wave w carries quarter w of every m-tile; e4m3 lo DMA: m-tiles
-  // (w/2) + 2r, half w%2
+  // hi and lo DMAs: wave w carries quarter w of every m-tile
   const _Float16* hsrc[NP];
 #pragma unroll
   for (int i = 0; i < NP; i++) {
@@ -915,13 +885,8 @@ __device__ __forceinline__ void gemm2_large_pass(const Problem& pb, const CHalf8
   const uint8_t* lsrc[kLoDma > 0 ? kLoDma : 1];
 #pragma unroll
   for (int r = 0; r < kLoDma; r++) {
-    if constexpr (kMode == kTwoTerms) {
-      const int p = row0 + min(16 * (i0 + (wave >> 1) + 2 * r) + lr, rows - 1);
-      lsrc[r] = ch.lo + (size_t)p * I + (4 * (wave & 1) + kg) * 16;
-    } else {
-      const int p = row0 + min(16 * (i0 + r) + lr, rows - 1);
-      lsrc[r] = reinterpret_cast<const uint8_t*>(ch.lo16 + (size_t)p * I + (4 * wave + kg) * 8);
-    }
+    const int p = row0 + min(16 * (i0 + r) + lr, rows - 1);
+    lsrc[r] = reinterpret_cast<const uint8_t*>(ch.lo16 + (size_t)p * I + (4 * wave + kg) * 8);
   }
   const float* ssrc = ch.scale + (size_t)(row0 + min(16 * i0 + 64 * wave + lane, rows - 1)) * KB;
 
@@ -934,14 +899,9 @@ __device__ __forceinline__ void gemm2_large_pass(const Problem& pb, const CHalf8
     for (int i = 0; i < NP; i++)
       __builtin_amdgcn_global_load_lds(hsrc[i] + (size_t)k * kBlock, st + i * 4096 + wave * 1024, 16, 0, 0);
 #pragma unroll
-    for (int r = 0; r < kLoDma; r++) {
-      if constexpr (kMode == kTwoTerms)
-        __builtin_amdgcn_global_load_lds(lsrc[r] + (size_t)k * kBlock,
-                                         st + L::kHi + ((wave >> 1) + 2 * r) * 2048 + (wave & 1) * 1024, 16, 0, 0);
-      else
-        __builtin_amdgcn_global_load_lds(lsrc[r] + (size_t)k * kBlock * 2, st + (NP + r) * 4096 + wave * 1024, 16,
-                                         0, 0);
-    }
+    for (int r = 0; r < kLoDma; r++)
+      __builtin_amdgcn_global_load_lds(lsrc[r] + (size_t)k * kBlock * 2, st + (NP + r) * 4096 + wave * 1024, 16, 0,
+                                       0);
     __builtin_amdgcn_global_load_lds(ssrc + k, st + L::kScales + wave * 256, 4, 0, 0);
     const uint8_t* b = bp + (size_t)k * kBlock;
     B[d][0] = load_w(b);
@@ -965,14 +925,8 @@ __device__ __forceinline__ void gemm2_large_pass(const Problem& pb, const CHalf8
                 lds_addr(st + L::kScales + (16 * i + 4 * kg) * 4), h0, h1, h2, h3, s4);
       const v8h ah[4] = {as_v8h(h0), as_v8h(h1), as_v8h(h2), as_v8h(h3)};
       const float4 sa = __builtin_bit_cast(float4, s4);
-      v8i al = {};
       v8h al16[4] = {};
       if constexpr (kMode == kTwoTerms) {
-        v4i x, y;
-        lds_read2(lds_addr(st + L::kHi + i * 2048 + ((2 * kg) * 16 + lr) * 16),
-                  lds_addr(st + L::kHi + i * 2048 + ((2 * kg + 1) * 16 + lr) * 16), x, y);
-        al = cat(x, y);
-      } else if constexpr (kMode == kPrecise) {
         const uint8_t* tl = st + (NP + i) * 4096;
         v4i l0, l1, l2, l3;
         lds_read4(lds_addr(tl + ((4 * kg + 0) * 16 + lr) * 16), lds_addr(tl + ((4 * kg + 1) * 16 + lr) * 16),
@@ -986,8 +940,7 @@ __device__ __forceinline__ void gemm2_large_pass(const Problem& pb, const CHalf8
 #pragma unroll
       for (int n = 0; n < 2; n++) {
         v4f p = mfma_f16_block(ah, b16[n], v4f{0.f, 0.f, 0.f, 0.f});
-        if constexpr (kMode == kTwoTerms) p = mfma16x16x128_exp<127 - 11>(al, B[d][n], p);
-        if constexpr (kMode == kPrecise) p = mfma_f16_block(al16, b16[n], p);
+        if constexpr (kMode == kTwoTerms) p = mfma_f16_block(al16, b16[n], p);
         acc[i][n][0] += p[0] * (sa.x * SW[d]);
         acc[i][n][1] += p[1] * (sa.y * SW[d]);
         acc[i][n][2] += p[2] * (sa.z * SW[d]);
@@ -1055,25 +1008,24 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
     const int2 uc = unit_at(pl.mbgroup, v, HB);
     const int mb = uniform(uc.x), hb = uniform(uc.y);
     const int4 blk = pl.mblocks[mb];
-    const int e = uniform(blk.x), flags = uniform(blk.w);
+    const int e = uniform(blk.x);
+    const bool two = uniform(pl.two_term[mb]) != 0;
     for (int s0 = 0; s0 < blk.z; s0 += 16 * MT) {
       const int row0 = uniform(blk.y + s0), rows = uniform(min(16 * MT, blk.z - s0));
       const int mvalid = (rows + 15) / 16;
-      if (flags & kFlagExactProducts) {
-        // GEMM1 wrote this block's lo term in f16
+      if (two) {
         for (int i0 = 0; i0 < mvalid; i0 += NP) {
           v4f acc[NP][2];
 #pragma unroll
           for (int i = 0; i < NP; i++) acc[i][0] = acc[i][1] = v4f{0.f, 0.f, 0.f, 0.f};
-          gemm2_large_pass<MT, NP, kPrecise>(pb, ch, ring, e, row0, rows, hb, i0, acc);
+          gemm2_large_pass<MT, NP, kTwoTerms>(pb, ch, ring, e, row0, rows, hb, i0, acc);
           gemm2_large_store<NP>(pl, obuf, H, row0, rows, hb, i0, acc);
         }
       } else {
         v4f acc[MT][2];
 #pragma unroll
         for (int i = 0; i < MT; i++) acc[i][0] = acc[i][1] = v4f{0.f, 0.f, 0.f, 0.f};
-        if (flags & kFlagTwoTermC) gemm2_large_pass<MT, MT, kTwoTerms>(pb, ch, ring, e, row0, rows, hb, 0, acc);
-        else gemm2_large_pass<MT, MT, kOneTerm>(pb, ch, ring, e, row0, rows, hb, 0, acc);
+        gemm2_large_pass<MT, MT, kOneTerm>(pb, ch, ring, e, row0, rows, hb, 0, acc);
         gemm2_large_store<MT>(pl, obuf, H, row0, rows, hb, 0, acc);
       }
     }
@@ -1081,24 +1033,23 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
 }
 
 // ------------------------------------------------------------------------------ GEMM2, 128-row m-blocks
-// For the 128-row blocks (one term of C, or two in blocks holding class 1 rows).  A workgroup of 8
-// wavefronts (one per CU, two per SIMD) owns one unit = (m-block, 256 output columns) and stages
-// C's hi term (f16), its lo term (e4m3, two-term blocks) and the W2 rows by DMA through a 3-stage
-// LDS ring, 64 K per stage.  Wavefront (wm, wn) = (w % 2, w / 2) computes rows 64 wm .. +63 x
-// output columns 64 wn .. +63 on the f16 MFMA 16x16x32 (W2 widened to f16 exactly; the lo term
-// widened with its 2^-11 scale, also exact, and chained onto the hi products).
+// For the 128-row blocks.  A workgroup of 8 wavefronts (one per CU, two per SIMD) owns one unit =
+// (m-block, 256 output columns) and stages C's hi term (f16), in blocks GEMM1 flagged also its lo
+// term (f16), and the W2 rows by DMA through a 3-stage LDS ring, 64 K per stage.  Wavefront
+// (wm, wn) = (w % 2, w / 2) computes rows 64 wm .. +63 x output columns 64 wn .. +63 on the f16
+// MFMA 16x16x32 (W2 widened to f16 exactly; the lo term's products chained onto the hi ones).
+// The block's rows come through its row map (a mixed block keeps its exact-product rows in its
+// last m-tiles; GEMM2 treats them like the others).
 //
 // Within a 64-K stage, lane group kg of an MFMA operand holds k = 16 kg + 8 t + (0..7) for the
-// two 32-K MFMAs t = 0, 1 (the same order for both operands): its W2 and lo bytes are one
-// 16-byte chunk, its hi values two.
+// two 32-K MFMAs t = 0, 1 (the same order for both operands): its W2 bytes are one 16-byte
+// chunk, its hi (and lo) values two.
 //
-// LDS stage: hi [128 rows][128 B] (chunks swizzled by bg_key), e4m3 lo [128 rows][64 B], f16 lo
-// of up to 32 exact-product rows [32 rows][128 B] (bg_key), W2 [256 rows][64 B] (chunk c of row r
-// in slot c ^ bg_key4(r)), 128 row scales of C.
+// LDS stage: hi [128 rows][128 B] and lo [128 rows][128 B] (chunks swizzled by bg_key), W2
+// [256 rows][64 B] (chunk c of row r in slot c ^ bg_key4(r)), 128 row scales of C.
 constexpr int kB2Cols = 256;
 constexpr int kB2Hi = kBgRows * 128;
-constexpr int kB2LoE = kBgRows * 64;
-constexpr int kB2Lo = kB2LoE + 32 * 128;
+constexpr int kB2Lo = kBgRows * 128;
 constexpr int kB2W = kB2Cols * 64;
 constexpr int kB2Stage = kB2Hi + kB2Lo + kB2W + kBgRows * 4;
 constexpr int kB2Stages = 3;
@@ -1107,13 +1058,13 @@ constexpr int kB2Stages = 3;
 // bank groups of a 256-byte bank row, and any 8 (same row parity) of a 128-byte one.
 __device__ __forceinline__ int bg_key4(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
 
-// e4m3 x 16 -> two f16 x 8 (MFMA operand order k = 8t + 0..7), scaled exactly by 2^kExp
-__device__ __forceinline__ void widen16(const v4i& x, float scale, v8h& t0, v8h& t1) {
+// e4m3 x 16 -> two f16 x 8 (MFMA operand order k = 8t + 0..7), exactly
+__device__ __forceinline__ void widen16(const v4i& x, v8h& t0, v8h& t1) {
 #pragma unroll
   for (int w = 0; w < 4; w++) {
     const uint32_t word = (uint32_t)x[w];
-    const v2h lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, scale, false);
-    const v2h hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, scale, true);
+    const v2h lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.0f, false);
+    const v2h hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(word, 1.0f, true);
     v8h& t = w < 2 ? t0 : t1;
     const int o = 4 * (w & 1);
     t[o + 0] = lo[0];
@@ -1124,44 +1075,31 @@ __device__ __forceinline__ void widen16(const v4i& x, float scale, v8h& t0, v8h&
 }
 
 // One unit.  Wavefront (wm, wn) computes m-tiles NT wm .. NT wm + NT - 1 (NT = 4, 2 or 1 for
-// blocks of more than 64, 33..64 and at most 32 rows).  kMode: kOneTerm / kTwoTerms, kPrecise
-// (blocks of at most 32 exact-product rows, NT = 1, with C's hi and f16 lo terms, the lo rows
-// staged in the stage's lo region as [32 rows][128 B]).
-template <int kMode, int NT>
+// blocks whose rows reach past LDS row 64, 32, or not).  kTwo: C's lo term too.
+template <bool kTwo, int NT>
 __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
-                                               uint32_t ring_lds, const float* sw2_s, int e, int row0, int rows,
+                                               uint32_t ring_lds, const float* sw2_s, int e, const RowMap& rm,
                                                int hc, float* __restrict__ obuf, int* queues, int* next_s,
                                                int n_units) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
-  static_assert(kMode != kPrecise || NT == 1, "exact-product blocks hold at most 32 rows");
+  constexpr int kOps = kTwo ? 7 : 5;   // DMAs per wavefront and stage: hi 2, lo 2, W2 2, row scales 1
   const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
   const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
-  // DMA sources (per-lane byte offsets): hi rows 16w + 8q + (lane / 8), 8 slots per row; e4m3 lo
-  // rows 16w + (lane / 4), W2 rows 32w + 16q + (lane / 4), 4 slots per row; f16 lo rows
-  // 8 (w % 4) + (lane / 8); row scales 64 (w % 2) + lane
-  uint32_t hoff[2], loff = 0, woff[2];
+  // DMA sources (per-lane byte offsets): hi and lo rows 16w + 8q + (lane / 8), 8 slots per row;
+  // W2 rows 32w + 16q + (lane / 4), 4 slots per row; row scales 64 (w % 2) + lane
+  uint32_t hoff[2], woff[2];
 #pragma unroll
   for (int q = 0; q < 2; q++) {
     const int r = 16 * wave + 8 * q + (lane >> 3);
-    const int p = row0 + min(r, rows - 1);
-    hoff[q] = (uint32_t)p * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
-  }
-  if (kMode == kTwoTerms) {
-    const int r = 16 * wave + (lane >> 2);
-    const int p = row0 + min(r, rows - 1);
-    loff = (uint32_t)p * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(r))) * 16);
-  } else if (kMode == kPrecise) {
-    const int r = 8 * (wave & 3) + (lane >> 3);
-    const int p = row0 + min(r, rows - 1);
-    loff = (uint32_t)p * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
+    hoff[q] = (uint32_t)rm.src(r) * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
   }
 #pragma unroll
   for (int q = 0; q < 2; q++) {
     const int R = 32 * wave + 16 * q + (lane >> 2);
     woff[q] = (uint32_t)(hc * kB2Cols + R) * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(R))) * 16);
   }
-  const uint32_t soff = 4u * (uint32_t)((row0 + min(64 * (wave & 1) + lane, rows - 1)) * KB);
+  const uint32_t soff = 4u * (uint32_t)(rm.src(64 * (wave & 1) + lane) * KB);
   const uint8_t* wbase = pb.w2 + (size_t)e * H * I;
   auto issue = [&](int j) {
     const int k = min(j, KS - 1);
@@ -1169,15 +1107,17 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
     const uint8_t* hbase = reinterpret_cast<const uint8_t*>(ch.hi) + (size_t)k * 128;
 #pragma unroll
     for (int q = 0; q < 2; q++) dma_lds16_s(hoff[q], hbase, st + (16 * wave + 8 * q) * 128);
-    if (kMode == kTwoTerms) dma_lds16_s(loff, ch.lo + (size_t)k * 64, st + kB2Hi + 16 * wave * 64);
-    if (kMode == kPrecise)
-      dma_lds16_s(loff, reinterpret_cast<const uint8_t*>(ch.lo16) + (size_t)k * 128, st + kB2Hi + 8 * (wave & 3) * 128);
+    if (kTwo) {
+      const uint8_t* lbase = reinterpret_cast<const uint8_t*>(ch.lo16) + (size_t)k * 128;
 #pragma unroll
-    for (int q = 0; q < 2; q++) dma_lds16_s(woff[q], wbase + (size_t)k * 64, st + kB2Hi + kB2Lo + (32 * wave + 16 * q) * 64);
+      for (int q = 0; q < 2; q++) dma_lds16_s(hoff[q], lbase, st + kB2Hi + (16 * wave + 8 * q) * 128);
+    }
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+      dma_lds16_s(woff[q], wbase + (size_t)k * 64, st + kB2Hi + kB2Lo + (32 * wave + 16 * q) * 64);
     dma_lds4_s(soff, ch.scale + k / 2, st + kB2Hi + kB2Lo + kB2W + (wave & 1) * 256);
   };
-  // operand read offsets: hi (and f16 lo) chunks 2kg + t of row lr (bg_key), e4m3 lo / W2 chunk kg
-  // of row lr (bg_key4)
+  // operand read offsets: hi / lo chunks 2kg + t of row lr (bg_key), W2 chunk kg of row lr (bg_key4)
   const int rh0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
   const int rh1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
   const int rq = lr * 64 + ((kg ^ bg_key4(lr)) * 16);
@@ -1190,17 +1130,16 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
 #pragma unroll
     for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
   for (int j = 0; j < KS; j++) {
-    // one stage in flight past the current one: 5 (one term) or 6 operations per wavefront
+    // one stage in flight past the current one: kOps operations per wavefront
     static_assert(kB2Stages == 3, "wait count");
-    if (kMode == kOneTerm) MOEFP8_WAIT_VMCNT(5);
-    else MOEFP8_WAIT_VMCNT(6);
+    if constexpr (kOps == 5) MOEFP8_WAIT_VMCNT(5);
+    else MOEFP8_WAIT_VMCNT(7);
     barrier_lds();
     const uint8_t* st = ring + (j % kB2Stages) * kB2Stage;
     v8h b16[4][2];
 #pragma unroll
     for (int n = 0; n < 4; n++)
-      widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + kB2Lo + (64 * wn + 16 * n) * 64 + rq), 1.0f, b16[n][0],
-              b16[n][1]);
+      widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + kB2Lo + (64 * wn + 16 * n) * 64 + rq), b16[n][0], b16[n][1]);
     const float sw = sw2_s[(j / 2) * 2 + (wn >> 1)];
 #pragma unroll
     for (int i = 0; i < NT; i++) {
@@ -1209,12 +1148,9 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
       const v8h a0 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh0));
       const v8h a1 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh1));
       v8h l0 = {}, l1 = {};
-      if constexpr (kMode == kTwoTerms)
-        widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + t * 16 * 64 + rq), 1.0f / kLoScale, l0, l1);
-      if constexpr (kMode == kPrecise) {
-        const uint8_t* lt = st + kB2Hi + t * 16 * 128;
-        l0 = as_v8h(*reinterpret_cast<const v4i*>(lt + rh0));
-        l1 = as_v8h(*reinterpret_cast<const v4i*>(lt + rh1));
+      if constexpr (kTwo) {
+        l0 = as_v8h(*reinterpret_cast<const v4i*>(ht + kB2Hi + rh0));
+        l1 = as_v8h(*reinterpret_cast<const v4i*>(ht + kB2Hi + rh1));
       }
       const float4 sa = *reinterpret_cast<const float4*>(st + kB2Hi + kB2Lo + kB2W + (16 * t + 4 * kg) * 4);
       const float4 sc = {sa.x * sw, sa.y * sw, sa.z * sw, sa.w * sw};
@@ -1222,7 +1158,7 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
       for (int n = 0; n < 4; n++) {
         v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b16[n][0], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b16[n][1], p, 0, 0, 0);
-        if constexpr (kMode != kOneTerm) {
+        if constexpr (kTwo) {
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, b16[n][0], p, 0, 0, 0);
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, b16[n][1], p, 0, 0, 0);
         }
@@ -1242,144 +1178,6 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
     const int t = NT * wm + i;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const int row = 16 * t + 4 * kg + r;
-      if (row < rows) {
-        const int p = row0 + row;
-        const float w = pl.perm_w[p];
-#pragma unroll
-        for (int n = 0; n < 4; n++) obuf[(size_t)p * H + hc * kB2Cols + 64 * wn + 16 * n + lr] = acc[i][n][r] * w;
-      }
-    }
-  }
-}
-
-// One unit of a mixed block.  Its DMAs: C's hi rows, its e4m3 lo rows (kLoE: the block holds class
-// 1 rows), the f16 lo rows of its exact-product rows (staged after the e4m3 ones), W2 and the row
-// scales.  This wavefront computes NF m-tiles tf0 .. from hi (+ the e4m3 lo term when kLoE) and NX
-// m-tiles tx0 .. from hi + the f16 lo term, its half of the block's tiles (mixed_split).  (Kept
-// apart from gemm2_big_unit, whose K loop the compiler schedules worse in this general form.)
-template <bool kLoE, bool kLo16, int NF, int NX>
-__device__ __forceinline__ void gemm2_big_mixed_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
-                                               uint32_t ring_lds, const float* sw2_s, int e, const RowMap& rm,
-                                               int hc, int tf0, int tx0, float* __restrict__ obuf, int* queues,
-                                               int* next_s, int n_units) {
-  constexpr int NT = NF + NX;
-  static_assert(NT >= 1 && NT <= 4, "m-tiles per wavefront");
-  static_assert(NX == 0 || kLo16, "exact-product tiles need the f16 lo rows");
-  constexpr int kOps = 2 + (kLoE ? 1 : 0) + (kLo16 ? 1 : 0) + 2 + 1;   // DMAs per wavefront and stage
-  const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
-  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
-  const int wn = wave >> 1;
-  auto tile = [&](int i) { return i < NF ? tf0 + i : tx0 + (i - NF); };
-  // DMA sources (per-lane byte offsets): hi rows 16w + 8q + (lane / 8), 8 slots per row; e4m3 lo
-  // rows 16w + (lane / 4), W2 rows 32w + 16q + (lane / 4), 4 slots per row; f16 lo rows
-  // xfrom + 8 (w % 4) + (lane / 8); row scales 64 (w % 2) + lane
-  uint32_t hoff[2], loff = 0, xoff = 0, woff[2];
-#pragma unroll
-  for (int q = 0; q < 2; q++) {
-    const int r = 16 * wave + 8 * q + (lane >> 3);
-    hoff[q] = (uint32_t)rm.src(r) * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
-  }
-  if (kLoE) {
-    const int r = 16 * wave + (lane >> 2);
-    loff = (uint32_t)rm.src(r) * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(r))) * 16);
-  }
-  if (kLo16) {
-    const int i = 8 * (wave & 3) + (lane >> 3);
-    xoff = (uint32_t)rm.src(min(rm.xfrom + i, kBgRows - 1)) * (uint32_t)(2 * I) +
-           (uint32_t)((((lane & 7) ^ bg_key(i))) * 16);
-  }
-#pragma unroll
-  for (int q = 0; q < 2; q++) {
-    const int R = 32 * wave + 16 * q + (lane >> 2);
-    woff[q] = (uint32_t)(hc * kB2Cols + R) * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(R))) * 16);
-  }
-  const uint32_t soff = 4u * (uint32_t)(rm.src(64 * (wave & 1) + lane) * KB);
-  const uint8_t* wbase = pb.w2 + (size_t)e * H * I;
-  auto issue = [&](int j) {
-    const int k = min(j, KS - 1);
-    const uint32_t st = ring_lds + (uint32_t)((j % kB2Stages) * kB2Stage);
-    const uint8_t* hbase = reinterpret_cast<const uint8_t*>(ch.hi) + (size_t)k * 128;
-#pragma unroll
-    for (int q = 0; q < 2; q++) dma_lds16_s(hoff[q], hbase, st + (16 * wave + 8 * q) * 128);
-    if (kLoE) dma_lds16_s(loff, ch.lo + (size_t)k * 64, st + kB2Hi + 16 * wave * 64);
-    if (kLo16)
-      dma_lds16_s(xoff, reinterpret_cast<const uint8_t*>(ch.lo16) + (size_t)k * 128,
-                  st + kB2Hi + kB2LoE + 8 * (wave & 3) * 128);
-#pragma unroll
-    for (int q = 0; q < 2; q++)
-      dma_lds16_s(woff[q], wbase + (size_t)k * 64, st + kB2Hi + kB2Lo + (32 * wave + 16 * q) * 64);
-    dma_lds4_s(soff, ch.scale + k / 2, st + kB2Hi + kB2Lo + kB2W + (wave & 1) * 256);
-  };
-  // operand read offsets: hi (and f16 lo) chunks 2kg + t of row lr (bg_key), e4m3 lo / W2 chunk kg
-  // of row lr (bg_key4)
-  const int rh0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
-  const int rh1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
-  const int rq = lr * 64 + ((kg ^ bg_key4(lr)) * 16);
-
-  MOEFP8_WAIT_VMCNT(0);
-  for (int d = 0; d < kB2Stages - 1; d++) issue(d);
-  v4f acc[NT][4];
-#pragma unroll
-  for (int i = 0; i < NT; i++)
-#pragma unroll
-    for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < KS; j++) {
-    // one stage in flight past the current one: kOps operations per wavefront
-    static_assert(kB2Stages == 3, "wait count");
-    static_assert(kOps >= 5 && kOps <= 7, "wait count");
-    if constexpr (kOps == 5) MOEFP8_WAIT_VMCNT(5);
-    else if constexpr (kOps == 6) MOEFP8_WAIT_VMCNT(6);
-    else MOEFP8_WAIT_VMCNT(7);
-    barrier_lds();
-    const uint8_t* st = ring + (j % kB2Stages) * kB2Stage;
-    v8h b16[4][2];
-#pragma unroll
-    for (int n = 0; n < 4; n++)
-      widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + kB2Lo + (64 * wn + 16 * n) * 64 + rq), 1.0f, b16[n][0],
-              b16[n][1]);
-    const float sw = sw2_s[(j / 2) * 2 + (wn >> 1)];
-#pragma unroll
-    for (int i = 0; i < NT; i++) {
-      const int t = tile(i);
-      const uint8_t* ht = st + t * 16 * 128;
-      const v8h a0 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh0));
-      const v8h a1 = as_v8h(*reinterpret_cast<const v4i*>(ht + rh1));
-      v8h l0 = {}, l1 = {};
-      const bool lo_term = i >= NF || kLoE;
-      if (i < NF && kLoE)
-        widen16(*reinterpret_cast<const v4i*>(st + kB2Hi + t * 16 * 64 + rq), 1.0f / kLoScale, l0, l1);
-      if (i >= NF) {
-        const uint8_t* lt = st + kB2Hi + kB2LoE + (16 * t - rm.xfrom) * 128;
-        l0 = as_v8h(*reinterpret_cast<const v4i*>(lt + rh0));
-        l1 = as_v8h(*reinterpret_cast<const v4i*>(lt + rh1));
-      }
-      const float4 sa = *reinterpret_cast<const float4*>(st + kB2Hi + kB2Lo + kB2W + (16 * t + 4 * kg) * 4);
-      const float4 sc = {sa.x * sw, sa.y * sw, sa.z * sw, sa.w * sw};
-#pragma unroll
-      for (int n = 0; n < 4; n++) {
-        v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b16[n][0], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-        p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b16[n][1], p, 0, 0, 0);
-        if (lo_term) {
-          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, b16[n][0], p, 0, 0, 0);
-          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, b16[n][1], p, 0, 0, 0);
-        }
-        acc[i][n][0] += p[0] * sc.x;
-        acc[i][n][1] += p[1] * sc.y;
-        acc[i][n][2] += p[2] * sc.z;
-        acc[i][n][3] += p[3] * sc.w;
-      }
-    }
-    issue(j + kB2Stages - 1);
-  }
-  MOEFP8_WAIT_VMCNT(0);
-  // the workgroup's next unit, claimed now so that the atomic overlaps the epilogue
-  if (threadIdx.x == 0) *next_s = grab_unit(queues, n_units);
-#pragma unroll
-  for (int i = 0; i < NT; i++) {
-    const int t = tile(i);
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
       const int R = 16 * t + 4 * kg + r;
       if (rm.valid(R)) {
         const int p = rm.src(R);
@@ -1392,8 +1190,8 @@ __device__ __forceinline__ void gemm2_big_mixed_unit(const Problem& pb, const Pl
 }
 
 // Units (m-block, 256 output columns) over GEMM2's blocks.
-__global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Plan pl, CHalf8 ch,
-                                                                 float* __restrict__ obuf) {
+__global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm2_big_kernel(
+    Problem pb, Plan pl, CHalf8 ch, float* __restrict__ obuf) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kB2Stages * kB2Stage];
   __shared__ float sw2_s[2 * kBigMaxKB];
   const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock, HC = H / kB2Cols;
@@ -1408,6 +1206,7 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
     const int mb = uniform(uc.x), hc = uniform(uc.y);
     const int4 blk = pl.mblocks[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
+    const bool two = uniform(pl.two_term[mb]) != 0;
     // the previous unit's readers are done with the ring and sw2_s, and every thread has read next_s
     __syncthreads();
     // W2 block scales of the unit's two 128-column blocks, per 128-K block
@@ -1417,48 +1216,51 @@ __global__ __launch_bounds__(kBgThreads, 1) void gemm2_big_kernel(Problem pb, Pl
     }
     __syncthreads();
     const RowMap rm = row_map(row0, rows, flags);
-    const int wm = wave_index() & 1;
-#define MOEFP8_G2_UNIT(LOE, LO16, NF, NX, TF0, TX0)                                                         \
-  gemm2_big_mixed_unit<LOE, LO16, NF, NX>(pb, pl, ch, ring, ring_lds, sw2_s, e, rm, hc, TF0, TX0, obuf, queues, \
-                                          &next_s, n_units)
-#define MOEFP8_G2_REG(MODE, NT) \
-  gemm2_big_unit<MODE, NT>(pb, pl, ch, ring, ring_lds, sw2_s, e, row0, rows, hc, obuf, queues, &next_s, n_units)
-    if (flags & kFlagMixed) {
-      const TileSplit ts = mixed_split(rm, wm);
-      const int nf = uniform(ts.nf), tf0 = uniform(ts.tf0), tx0 = uniform(ts.tx0);
-#define MOEFP8_G2_MIXED(LOE)                                      \
-  if (ts.nx == 0) {                                               \
-    if (nf == 1) MOEFP8_G2_UNIT(LOE, true, 1, 0, tf0, 0);         \
-    else if (nf == 2) MOEFP8_G2_UNIT(LOE, true, 2, 0, tf0, 0);    \
-    else if (nf == 3) MOEFP8_G2_UNIT(LOE, true, 3, 0, tf0, 0);    \
-    else MOEFP8_G2_UNIT(LOE, true, 4, 0, tf0, 0);                 \
-  } else {                                                        \
-    if (nf == 0) MOEFP8_G2_UNIT(LOE, true, 0, 1, 0, tx0);         \
-    else if (nf == 1) MOEFP8_G2_UNIT(LOE, true, 1, 1, tf0, tx0);  \
-    else if (nf == 2) MOEFP8_G2_UNIT(LOE, true, 2, 1, tf0, tx0);  \
-    else MOEFP8_G2_UNIT(LOE, true, 3, 1, tf0, tx0);               \
-  }
-      if (flags & kFlagTwoTermC) {
-        MOEFP8_G2_MIXED(true)
-      } else {
-        MOEFP8_G2_MIXED(false)
-      }
-#undef MOEFP8_G2_MIXED
-    } else if (flags & kFlagExactProducts) MOEFP8_G2_REG(kPrecise, 1);
-    else if (flags & kFlagTwoTermC) {
-      if (rows <= 32) MOEFP8_G2_REG(kTwoTerms, 1);
-      else if (rows <= 64) MOEFP8_G2_REG(kTwoTerms, 2);
-      else MOEFP8_G2_REG(kTwoTerms, 4);
+    // LDS rows in use: [0, rows), and a mixed block's exact rows up to row 127
+    const int top = (flags & kFlagMixed) ? kBgRows : rows;
+#define MOEFP8_G2_UNIT(TWO, NT) \
+  gemm2_big_unit<TWO, NT>(pb, pl, ch, ring, ring_lds, sw2_s, e, rm, hc, obuf, queues, &next_s, n_units)
+    if (two) {
+      if (top <= 32) MOEFP8_G2_UNIT(true, 1);
+      else if (top <= 64) MOEFP8_G2_UNIT(true, 2);
+      else MOEFP8_G2_UNIT(true, 4);
     } else {
-      if (rows <= 32) MOEFP8_G2_REG(kOneTerm, 1);
-      else if (rows <= 64) MOEFP8_G2_REG(kOneTerm, 2);
-      else MOEFP8_G2_REG(kOneTerm, 4);
+      if (top <= 32) MOEFP8_G2_UNIT(false, 1);
+      else if (top <= 64) MOEFP8_G2_UNIT(false, 2);
+      else MOEFP8_G2_UNIT(false, 4);
     }
-#undef MOEFP8_G2_REG
 #undef MOEFP8_G2_UNIT
     // next_s is written
     __syncthreads();
   }
+}
+
+// ------------------------------------------------------------------------------------------ flags
+// GEMM2's precision flag of m-block g: two terms of C where the permutation's estimate put class 1
+// rows (kFlagTwoTermC), or where one of the block's rows needs them by its measured C
+// (needs_two_terms on the row's max |C| per 128 columns, 448 x the scales GEMM1 wrote).  A launch
+// of its own between the GEMMs: the same test inside GEMM1's epilogue made the compiler schedule
+// GEMM1's K loop worse.
+__global__ __launch_bounds__(256) void c_flags_kernel(Plan pl, CHalf8 ch, int I) {
+  const int g = blockIdx.x;
+  if (g >= pl.info[2]) return;
+  const int4 blk = pl.mblocks[g];
+  // a mixed block's exact rows follow its regular rows
+  const int n = blk.z + ((blk.w & kFlagMixed) ? (blk.w >> kMixedShift) : 0);
+  const int NCB = I / kBlock;
+  const float sigma2 = pl.esig[2 * blk.x + 1], sqrt_i = sqrtf((float)I);
+  bool need = (blk.w & kFlagTwoTermC) != 0;
+  for (int i = threadIdx.x; i < n * NCB; i += blockDim.x) {
+    const int p = blk.y + i / NCB;
+    need |= needs_two_terms(pl.perm_w[p], sigma2, 448.0f * ch.scale[(size_t)p * NCB + i % NCB], sqrt_i);
+  }
+  need = __syncthreads_or(need);
+  if (threadIdx.x == 0) pl.two_term[g] = need ? 1 : 0;
+}
+
+void launch_c_flags(const Plan& pl, const CHalf8& ch, int I, int max_blocks, hipStream_t stream) {
+  if (max_blocks <= 0) return;
+  hipLaunchKernelGGL(c_flags_kernel, dim3(max_blocks), dim3(256), 0, stream, pl, ch, I);
 }
 
 // ------------------------------------------------------------------------------------------ launch

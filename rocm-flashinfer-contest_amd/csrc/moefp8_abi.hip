@@ -43,7 +43,7 @@ int large_rows_b(int64_t T, int E, int H, int I) { return large_big(T, E, H, I) 
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
   size_t tok_a2, esig, mtiles, counters, c16, c16_scale, gbuf, obuf;
-  size_t canon_token, bcnt, ccnt, mblocks, mbgroup, queues, c_hi, c_lo, c_lo16, c_scale;
+  size_t canon_token, bcnt, ccnt, mblocks, mbgroup, two_term, queues, c_hi, c_lo16, c_scale;
   size_t total;
   int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks, n_counters1, n_counters;
   int nblk;
@@ -83,10 +83,11 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
     const int64_t kbmax = (H > I ? H : I) / kBlock, smin = (kbmax + 63) / 64;
     L.rows_cap = pmax * smin > r8 ? pmax * smin : r8;
     L.mtiles = take((size_t)L.max_mtiles * 16);
-    // arrival counters: per (m-tile, 128 C columns) for GEMM1, then per output column block
+    // arrival counters: per (m-tile, 128 C columns) for GEMM1, then per output column block,
+    // then GEMM2's precision flag per m-tile (all zeroed by the routing kernel)
     L.n_counters1 = L.max_mtiles * (I / kBlock);
     L.n_counters = L.n_counters1 + H / (16 * decode_unit_groups());
-    L.counters = take((size_t)L.n_counters * 4);
+    L.counters = take((size_t)(L.n_counters + L.max_mtiles) * 4);
     L.gbuf = take((size_t)L.rows_cap * 2 * I * 4);
     L.c16 = take((size_t)L.c_plane * 2 * 2);
     L.c16_scale = take((size_t)pmax * (I / kBlock) * 4);
@@ -94,7 +95,7 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
     L.total = o;
     return L;
   }
-  // large T: permutation scratch and tables, C (f16 hi, e4m3 or f16 lo, fp32 scales), O [pmax][H] fp32
+  // large T: permutation scratch and tables, C (f16 hi and lo, fp32 scales), O [pmax][H] fp32
   L.rows_cap = pmax;
   L.nblk = permute_large_blocks(T);
   const int ra = large_rows_a(T, E_local, H, I), rb = large_rows_b(T, E_local, H, I);
@@ -106,9 +107,9 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.ccnt = take((size_t)L.nblk * E_local * 4);
   L.mblocks = take((size_t)L.max_blocks * 16);
   L.mbgroup = take((size_t)L.max_blocks * 8);
+  L.two_term = take((size_t)L.max_blocks * 4);
   L.queues = take((size_t)kUnitQueues * kQueueStride * 4);
   L.c_hi = take((size_t)pmax * I * 2);
-  L.c_lo = take((size_t)pmax * I);
   L.c_lo16 = take((size_t)pmax * I * 2);
   L.c_scale = take((size_t)pmax * (I / kBlock) * 4);
   L.obuf = take((size_t)pmax * H * 4);
@@ -324,6 +325,8 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
   pl.canon_token = pl.perm_token;
   pl.counters = nullptr;
   pl.counters2 = nullptr;
+  pl.esig = reinterpret_cast<const float*>(ws + L.esig);
+  pl.two_term = nullptr;
   pl.shared = a->shared_output;
   pl.shared_dt = a->shared_dtype;
   pl.out_f32 = a->output_f32;
@@ -356,6 +359,7 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
     pl.mtiles = reinterpret_cast<const int4*>(ws + L.mtiles);
     pl.counters = reinterpret_cast<int*>(ws + L.counters);
     pl.counters2 = pl.counters + L.n_counters1;
+    pl.two_term = pl.counters + L.n_counters;
     DecodePlanArgs da;
     da.topk_ids = topk_ids;
     da.topk_w = topk_w;
@@ -376,7 +380,7 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
     da.mtiles = const_cast<int4*>(pl.mtiles);
     mark(0);
     launch_route(a->routing_logits, a->logits_dtype, a->routing_bias, a->bias_dtype, T, a->routed_scaling_factor,
-                 topk_ids, topk_w, &mag, pl.counters, (int)L.n_counters, s);
+                 topk_ids, topk_w, &mag, pl.counters, (int)(L.n_counters + L.max_mtiles), s);
     mark(1);
     mark(2);   // the permutation is rebuilt by every GEMM1 workgroup: empty permute stage
     float* gbuf = reinterpret_cast<float*>(ws + L.gbuf);
@@ -425,9 +429,9 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
   pl.mblocks = pa.mblocks;
   pl.mbgroup = pa.mbgroup;
   pl.queues = pa.queues;
+  pl.two_term = reinterpret_cast<int*>(ws + L.two_term);
   CHalf8 ch;
   ch.hi = reinterpret_cast<_Float16*>(ws + L.c_hi);
-  ch.lo = ws + L.c_lo;
   ch.lo16 = reinterpret_cast<_Float16*>(ws + L.c_lo16);
   ch.scale = reinterpret_cast<float*>(ws + L.c_scale);
   float* obuf = reinterpret_cast<float*>(ws + L.obuf);
@@ -443,7 +447,9 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
     launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks * (I / kBlock)), s);
   }
   mark(3);
-  mark(4);   // SwiGLU is GEMM1's epilogue here: empty activation stage
+  // GEMM2's precision per m-block from the C that GEMM1 wrote (the activation stage)
+  launch_c_flags(pl, ch, I, (int)L.max_blocks, s);
+  mark(4);
   if (big) {
     launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks * (H / 256)), s);
   } else {

@@ -66,14 +66,13 @@ __device__ __forceinline__ void split_f16(float x, float inv, _Float16& hi, _Flo
 }
 
 // Predicted size of a pair's output row (rms of routing-weighted GEMM2 output) from
-// the token's squared hidden-state norm and the expert's weight-magnitude estimates;
-// pairs above kPreciseRms run the exact-product path.  rms(G1) ~ ||A|| s13,
-// rms(C) ~ 0.7 rms(G1)^2, rms(O) ~ rms(C) s2 sqrt(I).
+// the token's squared hidden-state norm and the expert's weight-magnitude estimates:
+// rms(G1) ~ ||A|| s13, rms(C) ~ 0.7 rms(G1)^2, rms(O) ~ rms(C) s2 sqrt(I) (it over-estimates
+// the measured rms ~7x).  Used before GEMM1, where only the inputs are known: pairs above
+// kPreciseRms take GEMM1's exact-product path (the fp8 MFMA's adder error is relative to
+// sum |a w|, which this estimate tracks), and pairs above kOneTermRms are grouped together inside
+// their expert and take two terms of C in GEMM2 (kFlagTwoTermC).
 constexpr float kPreciseRms = 96.0f;
-
-// Per-pair flag bits.  The small-T GEMM2 multiplies C's f16 hi term alone (relative
-// error 2^-11 per element, ~2^-12 rms of the output) unless the predicted output rms
-// exceeds kOneTermRms; the predictor overestimates the measured rms about 7x.
 constexpr float kOneTermRms = 8.0f;
 constexpr uint8_t kFlagExactProducts = 1;
 constexpr uint8_t kFlagTwoTermC = 2;
@@ -81,6 +80,29 @@ constexpr uint8_t kFlagTwoTermC = 2;
 // count in the bits from kMixedShift up.
 constexpr int kFlagMixed = 4;
 constexpr int kMixedShift = 8;
+
+// GEMM2's precision of C, also checked on C itself, so that inputs the estimate above misjudges
+// (hidden rows aligned with an expert's W13 rows, where G1 is ~sqrt(H) times the estimate) still
+// get two terms.  GEMM1 knows, per pair and 128-column block cb, amax_cb = max |C| over the block
+// (it scales C's split by it); the test is
+//   q = |w| * sigma2 * sqrt(I) * amax_cb > kOneTermQ,
+// sigma2 the expert's W2 entry scale (448 * largest block scale / 3).  Since
+// ||C||_2^2 <= sum_cb 128 amax_cb^2 <= I max_cb amax_cb^2, the largest q over the blocks bounds
+// |w| ||C||_2 sigma2, the rms of the pair's routing-weighted output row for W2 entries of rms
+// sigma2.  C's f16 hi term rounds each element by at most 2^-11 relative (a block's largest
+// element, scaled to 448, exactly), so one term leaves an output error of rms at most
+// 2^-11 / sqrt(3) * q (C flat across its elements); on the lognormal T = 8192 benchmark
+// workload the one-term error of a pair measures at most 2.1e-5 * q in rms and 9.1e-5 * q at its
+// worst column.  There every pair the estimate keeps at one term has q <= 37 (99% <= 23), so
+// kOneTermQ sits above them: the measured test only adds two-term blocks where the estimate
+// fails.  An m-block (m-tile at small T) holding a pair with q > kOneTermQ takes C's f16 lo term
+// (22 significant bits in all); the flag is set, never cleared, by whichever unit finds such a
+// pair, so it does not depend on the order in which units finish.
+constexpr float kOneTermQ = 32.0f;
+
+__device__ __forceinline__ bool needs_two_terms(float w, float sigma2, float amax, float sqrt_i) {
+  return fabsf(w) * sigma2 * sqrt_i * amax > kOneTermQ;
+}
 
 __device__ __forceinline__ float predicted_output_rms(float a2, float w, float s13, float s2, float sqrt_i) {
   return fabsf(w) * 0.7f * a2 * s13 * s13 * s2 * sqrt_i;
@@ -171,37 +193,6 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t byte) {
 // fp32 -> OCP e4m3fn, round to nearest even; |x| must be <= 448 (callers clamp).
 __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x, 0.0f, 0, false) & 0xffu;
-}
-
-// Multi-term e4m3 representation of GEMM2's activations.  With v = x * inv
-// (|v| <= 448 after the per-block scale) the terms are q_0 = e4m3(v) and
-// q_k = e4m3(16^k * (v - sum_{j<k} q_j 16^-j)), so v ~ sum_k q_k 16^-k.  Every
-// residual stays inside the e4m3 range (|residual| <= half an ulp of the
-// previous term) and each term adds ~4 more significant bits: 2 terms ~2^-8,
-// 3 terms ~2^-12, 4 terms ~2^-16 relative error.
-constexpr int kMaxTerms = 4;
-// Output-error budget of one (row, 128-column block) of C: the smallest term
-// count k with 2^(-4k) * ||C_block||_2 * |routing weight| * max|W2 block column|
-// <= kTermTau is used.
-constexpr float kTermTau = 4.0e-3f;
-
-__device__ __forceinline__ void split_terms(float x, float inv, uint32_t (&q)[kMaxTerms]) {
-  float r = fminf(fmaxf(x * inv, -448.0f), 448.0f);
-#pragma unroll
-  for (int k = 0; k < kMaxTerms; k++) {
-    q[k] = f32_to_e4m3(r);
-    r = (r - e4m3_to_f32(q[k])) * 16.0f;
-  }
-}
-
-__device__ __forceinline__ int terms_needed(float gain) {
-  return gain * 0x1p-8f <= kTermTau ? 2 : (gain * 0x1p-12f <= kTermTau ? 3 : 4);
-}
-
-// Term k of the split: A scaled by 2^(-4k) exactly (E8M0 exponent 127 - 4k) in the MFMA itself.
-__device__ __forceinline__ v4f mfma16x16x128_term(const v8i& a, const v8i& b, const v4f& c, int k) {
-  if (k == 0) return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127 - 4 * k, 0, 127);
 }
 
 // Per-block scale of the split: amax -> (inv = 448/amax, scale = amax/448).

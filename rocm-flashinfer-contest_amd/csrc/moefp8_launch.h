@@ -69,6 +69,10 @@ struct Plan {
   const int* canon_token;     // token of each pair in canonical (expert, token) order
   int* counters;              // small T: arrivals per (m-tile, 128 C columns), zeroed by the routing
   int* counters2;             // small T: arrivals per 64 output columns, zeroed by the routing
+  const float* esig;          // [E, 2] W13 and W2 entry scale estimates of each local expert (routing)
+  int* two_term;              // GEMM2's precision flags from measured C (needs_two_terms): per m-tile
+                              // at small T (zeroed by the routing, set by GEMM1), per m-block at large T
+                              // (written by the flags launch between the GEMMs)
   const void* shared;         // optional [T, H] rows added before the bf16 rounding (NULL: none)
   int shared_dt;              // 0 fp32, 1 bf16
   int out_f32;                // output in fp32 (the sum before its bf16 rounding) instead of bf16
@@ -132,11 +136,11 @@ struct LargePermArgs {
 void launch_permute_large(const LargePermArgs& args, hipStream_t stream);
 int permute_large_blocks(int64_t T);
 
-// C between the large-T GEMMs: hi = f16(C/s), lo = e4m3(2^11 (C/s - hi)), s per (pair, 128 cols).
+// C between the large-T GEMMs: hi = f16(C/s), lo16 = f16(C/s - hi), s = max |C| / 448 per
+// (pair, 128 columns).  GEMM2 reads lo16 only in m-blocks flagged two_term.
 struct CHalf8 {
   _Float16* hi;     // [Pmax][I]
-  uint8_t* lo;      // [Pmax][I], e4m3 lo term (m-blocks without exact-product pairs)
-  _Float16* lo16;   // [Pmax][I], f16 lo term (m-blocks with exact-product pairs)
+  _Float16* lo16;   // [Pmax][I]
   float* scale;     // [Pmax][I/128]
 };
 int large_grid();
@@ -148,6 +152,8 @@ void launch_gemm1_large(const Problem& pb, const Plan& pl, const CHalf8& ch, int
 constexpr int kBigRows = 128;
 constexpr int kBigMaxKB = 64;   // H <= 8192
 void launch_gemm1_big(const Problem& pb, const Plan& pl, const CHalf8& ch, int max_units, hipStream_t stream);
+// GEMM2's precision flags (Plan::two_term) of the blocks [0, info[2]) from GEMM1's output
+void launch_c_flags(const Plan& pl, const CHalf8& ch, int I, int max_blocks, hipStream_t stream);
 // GEMM2 over the blocks [0, info[2]), taken 16 * mt rows at a time
 void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
                         hipStream_t stream);

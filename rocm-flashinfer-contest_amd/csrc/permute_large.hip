@@ -23,13 +23,14 @@ constexpr int kBlkWaves = kBlkTokens / kWave;
 constexpr int kClasses = 3;
 constexpr int kScanThreads = 1024;
 
-// 0: one f16 term of C is enough; 1: two terms; 2: two terms and exact GEMM1 products.
+// 0: one f16 term of C is enough; 1: two terms; 2: two terms and exact GEMM1 products (GEMM2
+// may still take two terms for a class 0 block, from the C that GEMM1 writes).
 __device__ __forceinline__ int magnitude_class(float pred) {
   return pred > kPreciseRms ? 2 : (pred > kOneTermRms ? 1 : 0);
 }
 
-__device__ __forceinline__ uint8_t class_flags(int c) {
-  return c == 0 ? 0 : (c == 1 ? kFlagTwoTermC : (uint8_t)(kFlagTwoTermC | kFlagExactProducts));
+__device__ __forceinline__ int class_flags(int c) {
+  return c == 0 ? 0 : (c == 1 ? kFlagTwoTermC : kFlagTwoTermC | kFlagExactProducts);
 }
 
 // Does an expert with n01 class 0/1 rows and n2 exact-product rows fold the latter into its last
@@ -199,12 +200,12 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
     const int ba = (c01 + a.rows_a - 1) / a.rows_a;
     if (j < ba) {
       const int r0 = j * a.rows_a, rows = min(a.rows_a, c01 - r0);
-      int flags = r0 + rows > c0 ? (int)class_flags(1) : 0;
+      int flags = r0 + rows > c0 ? class_flags(1) : 0;
       if (j == ba - 1 && folds_exact(a, c01, n - c01)) flags |= kFlagMixed | ((n - c01) << kMixedShift);
       a.mblocks[g] = int4{e, eoff[e] + r0, rows, flags};
     } else {
       const int r0 = c01 + (j - ba) * a.rows_b;
-      a.mblocks[g] = int4{e, eoff[e] + r0, min(a.rows_b, n - r0), (int)class_flags(2)};
+      a.mblocks[g] = int4{e, eoff[e] + r0, min(a.rows_b, n - r0), class_flags(2)};
     }
     a.mbgroup[g] = int2{eb1[e], eb1[e + 1] - eb1[e]};
   }

@@ -1,0 +1,97 @@
+"""Parity on structured activations at the operator's full size (H=7168, I=2048, 32 local
+experts), where the per-pair output magnitude is far from what the token's hidden-state norm
+predicts:
+
+* aligned   -- a token's hidden row is built from the dequantised gate and up rows j of 2-3 of
+               the experts it routes to, so those experts' G1_j is ~sqrt(H) times the rms
+               estimate and C_j ~ 1e4 (the pair's output rows ~1e2), while ||a|| is ordinary;
+* outliers  -- 2-8 of the 7168 channels carry x100 values;
+* both, with every token routed to 8 local experts (forced logits), so that several large
+  pair rows meet in each token's sum and cancel in some columns.
+
+Bars as elsewhere: every element within atol 1e-2 / rtol 2e-2 of the oracle's fp32 output,
+an element that misses it re-evaluated for its token with fp64 accumulation."""
+import numpy as np
+import pytest
+import torch
+
+import moe_oracle as O
+import moe_fp8
+from moe_fp8 import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda:0")
+ATOL, RTOL = 1e-2, 2e-2
+E, H, I = 32, 7168, 2048
+
+
+@pytest.fixture(scope="module")
+def weights():
+    w = W.make_weights(device=DEV)
+    torch.cuda.synchronize()
+    return w, tuple(x.cpu() for x in w)
+
+
+def dequant_row(w13c, s13, e, r):
+    """fp32 row r of expert e's W13 (128x128 block scales)."""
+    q = O.decode_e4m3(w13c[e, r].view(torch.uint8).numpy())
+    return torch.from_numpy(q * np.repeat(s13[e, r // 128].numpy(), 128))
+
+
+def build(kind, T, seed, w_cpu):
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(T, 256, generator=g)
+    bias = (torch.randn(256, generator=g) * 0.1).to(torch.bfloat16)
+    chosen = torch.stack([torch.randperm(E, generator=g)[:8] for _ in range(T)])   # 8 local experts per token
+    logits.scatter_add_(1, chosen, torch.full((T, 8), 6.0))
+    x = torch.randn(T, H, generator=g)
+    w13c, s13 = w_cpu[0], w_cpu[1]
+    if kind in ("aligned", "both", "aligned_block"):
+        rows = 4 if kind == "aligned_block" else 1
+        for t in range(T):
+            n = 2 + t % 2
+            a = torch.zeros(H)
+            for e in chosen[t, :n].tolist():
+                # `rows` consecutive C columns j.. inside one 128-column block: only the block's
+                # largest element lands exactly on the split's 448, the others round in f16
+                j = int(torch.randint(0, I // 128, (1,), generator=g)) * 128 + int(torch.randint(0, 128 - rows, (1,), generator=g))
+                for r in range(rows):
+                    a += dequant_row(w13c, s13, e, j + r) + dequant_row(w13c, s13, e, I + j + r)
+            # the aligned part carries the row's norm; 0.1 of it is ordinary noise
+            x[t] = a * (float(x[t].norm()) / float(a.norm())) + 0.1 * x[t]
+    if kind == "amplified":
+        x *= torch.exp(torch.randn(T, 1, generator=g) * 1.5)         # log-normal row amplitudes
+    if kind in ("outliers", "both"):
+        for t in range(T):
+            ch = torch.randperm(H, generator=g)[: 2 + t % 7]
+            x[t, ch] *= 100.0
+    hs, hss = W.quantize_rows_1x128(x)
+    return logits, bias, hs, hss
+
+
+@pytest.mark.parametrize("kind", ["aligned", "aligned_block", "outliers", "both", "amplified"])
+@pytest.mark.parametrize("T", [48, 400])
+def test_structured_activations(weights, kind, T):
+    print(f"[structured] {kind} T={T}", flush=True)
+    w_dev, w_cpu = weights
+    act = build(kind, T, 7000 + T + len(kind), w_cpu)
+    out = moe_fp8.run(*(a.to(DEV) for a in act), *w_dev, 0, W.RSF)
+    torch.cuda.synchronize()
+    ref32, _ = O.moe_forward(*act, *w_cpu, 0, W.RSF)
+    got = out.float().cpu()
+    print(f"  max |ref| {float(ref32.abs().max()):.1f}, max err {float((got - ref32).abs().max()):.4f}", flush=True)
+    miss = (got - ref32).abs() > ATOL + RTOL * ref32.abs()
+    bad = []
+    tokens = sorted({t for t, _ in torch.nonzero(miss).tolist()})
+    for t in tokens:
+        one = (act[0][t:t + 1], act[1], act[2][t:t + 1], act[3][:, t:t + 1].contiguous())
+        o64, _ = O.moe_forward(*one, *w_cpu, 0, W.RSF, accumulate=torch.float64)
+        for h in torch.nonzero(miss[t]).flatten().tolist():
+            exact = float(o64[0, h])
+            if abs(float(got[t, h]) - exact) > ATOL + RTOL * abs(exact):
+                bad.append((t, h, float(ref32[t, h]), exact, float(got[t, h])))
+    print(f"  {int(miss.sum())} elements miss the fp32 oracle's bar, {len(bad)} the fp64 value's", flush=True)
+    for b in bad[:10]:
+        print("   t=%d h=%d fp32 %.5f fp64 %.5f HIP %.5f" % b, flush=True)
+    assert not bad
