@@ -60,21 +60,22 @@ __device__ __forceinline__ DecUnit decode_unit(int u, int S, int NCB) {
   return DecUnit{rest / S, rest % S, u - rest * NCB};
 }
 
-// LDS stage of GEMM1: 16 activation rows x 128 e4m3 bytes stored [16-byte chunk][row]
-// (the MFMA operand read, 2 x 16 bytes per lane, is then conflict-free) and the 16 row
-// scales.
+// LDS stage of GEMM1: 16 activation rows x 128 e4m3 bytes (chunk c of row r in slot
+// c ^ slot_key8(r)) and the 16 row scales.
 struct alignas(16) G1Stage {
-  uint8_t a[8 * 16 * 16];
+  uint8_t a[16 * kBlock];
   float sa[16];
 };
 
 // Activation rows of an m-tile with at most kPreRows rows, staged once per unit for its
 // whole K-range (<= kPreMaxKB K-blocks) with their scales: the weight stream then runs
 // without a barrier per K step.  In decode most m-tiles hold one or two pairs.  Rows are
-// 64 bytes longer than their data, so equal offsets of different rows fall 16 banks apart.
+// padded (GEMM1 80 bytes, GEMM2 16) so that the operand reads of the <= 4 rows (GEMM1: 32
+// bytes per lane group, GEMM2: 64) fall on distinct 16-byte bank groups whether the LDS serves
+// 8, 16 or 32 lanes at a time.
 constexpr int kPreRows = 4;
 constexpr int kPreMaxKB = 28;
-constexpr int kPre1RowBytes = kPreMaxKB * kBlock + 64;
+constexpr int kPre1RowBytes = kPreMaxKB * kBlock + 80;
 struct alignas(16) G1Pre {
   uint8_t a[kPreRows * kPre1RowBytes];
   float sa[kPreMaxKB][kPreRows];
@@ -82,15 +83,16 @@ struct alignas(16) G1Pre {
 
 // GEMM2's staged rows: C's f16 hi term, <= kPre2MaxKB K-blocks of 128 columns per unit.
 constexpr int kPre2MaxKB = 16;
-constexpr int kPre2RowBytes = kPre2MaxKB * kBlock * 2 + 64;
+constexpr int kPre2RowBytes = kPre2MaxKB * kBlock * 2 + 16;
 struct alignas(16) G2Pre {
   uint8_t a[kPreRows * kPre2RowBytes];
   float sa[kPre2MaxKB][kPreRows];
 };
 
-// LDS stage of GEMM2: 16 rows of C's f16 hi term x 128 columns, same chunk-major order.
+// LDS stage of GEMM2: 16 rows of C's f16 hi term x 128 columns (256 bytes, chunk c of row r in
+// slot c ^ slot_key16(r)) and the 16 row scales.
 struct alignas(16) G2Stage {
-  _Float16 a[16 * 16 * 8];
+  uint8_t a[16 * 2 * kBlock];
   float sa[16];
 };
 
@@ -212,15 +214,14 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
       // weights as whole 128-byte lines: lane l loads 16-byte chunk l%8 of rows l/8 and
       // 8 + l/8 of each K-block, then the wavefront transposes the block through its LDS
       // buffer into the MFMA layout (16 rows x 64 bytes per load instruction in that layout
-      // streams ~7% slower, measured).  Chunk c of row r sits at slot c ^ ((r >> 1) & 7):
-      // both the line-order writes and the MFMA-order reads are bank-conflict free.
+      // streams ~7% slower, measured).  Chunk c of row r sits at slot c ^ slot_key8(r).
       const int wr = lane >> 3, wc = lane & 7;
       const uint8_t* wsrc = pb.w13 + ((size_t)e * I2 + cg * 16 + wr) * H + (size_t)kb0 * kBlock + wc * 16;
       uint8_t* const tb = wtr[wave];
-      uint8_t* const tw0 = tb + wr * kBlock + ((wc ^ (wr >> 1)) & 7) * 16;
-      uint8_t* const tw1 = tb + (wr + 8) * kBlock + ((wc ^ ((wr + 8) >> 1)) & 7) * 16;
-      const uint8_t* const trx = tb + lr * kBlock + (((2 * kg) ^ (lr >> 1)) & 7) * 16;
-      const uint8_t* const try_ = tb + lr * kBlock + (((2 * kg + 1) ^ (lr >> 1)) & 7) * 16;
+      uint8_t* const tw0 = tb + wr * kBlock + (wc ^ slot_key8(wr)) * 16;
+      uint8_t* const tw1 = tb + (wr + 8) * kBlock + (wc ^ slot_key8(wr + 8)) * 16;
+      const uint8_t* const trx = tb + lr * kBlock + ((2 * kg) ^ slot_key8(lr)) * 16;
+      const uint8_t* const try_ = tb + lr * kBlock + ((2 * kg + 1) ^ slot_key8(lr)) * 16;
       v4i B0[kDecDepth], B1[kDecDepth];
       auto load = [&](int d, int j) {
         const uint8_t* p = wsrc + (size_t)min(j, n - 1) * kBlock;
@@ -289,7 +290,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
     } else if (!(flags & kFlagExactProducts)) {
       constexpr int kStepDepth = 2;   // (register budget shared with the staged path)
       // carriers: waves 0/1 load rows 8q .. 8q + 7 of the activation block as whole 128-byte
-      // lines (lane l: row 8q + l/8, 16-byte chunk l%8) and publish them chunk-major; wave 0's
+      // lines (lane l: row 8q + l/8, 16-byte chunk l%8) and publish them to the stage; wave 0's
       // lanes < 16 publish the scale of row lane.  Waves 2/3 issue as many loads, from one
       // fixed line (loads under a branch would make the compiler's wait counting fall back to
       // draining all of them).  Activation loads in the MFMA layout by every wavefront (16
@@ -313,11 +314,11 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
       };
       auto step = [&](int d, int j) {
         G1Stage& st = ring[j & 1];
-        if (wave < 2) *reinterpret_cast<v4i*>(st.a + ((lane & 7) * 16 + ar) * 16) = AR[d];
+        if (wave < 2) *reinterpret_cast<v4i*>(st.a + ar * kBlock + ((lane & 7) ^ slot_key8(ar)) * 16) = AR[d];
         if (wave == 0 && lane < 16) st.sa[lane] = SR[d];
         __syncthreads();
-        const v4i x = *reinterpret_cast<const v4i*>(st.a + ((2 * kg) * 16 + lr) * 16);
-        const v4i y = *reinterpret_cast<const v4i*>(st.a + ((2 * kg + 1) * 16 + lr) * 16);
+        const v4i x = *reinterpret_cast<const v4i*>(st.a + lr * kBlock + ((2 * kg) ^ slot_key8(lr)) * 16);
+        const v4i y = *reinterpret_cast<const v4i*>(st.a + lr * kBlock + ((2 * kg + 1) ^ slot_key8(lr)) * 16);
         const float4 sa = *reinterpret_cast<const float4*>(st.sa + 4 * kg);
         const float sw = readlane_f32(swv, j);
         const v4f p = mfma16x16x128(__builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7), B[d],
@@ -512,10 +513,10 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       const int wr = lane >> 3, wc = lane & 7;
       const uint8_t* wsrc = pb.w2 + ((size_t)e * H + cg * 16 + wr) * I + (size_t)kb0 * kBlock + wc * 16;
       uint8_t* const tb = wtr[wave];
-      uint8_t* const tw0 = tb + wr * kBlock + ((wc ^ (wr >> 1)) & 7) * 16;
-      uint8_t* const tw1 = tb + (wr + 8) * kBlock + ((wc ^ ((wr + 8) >> 1)) & 7) * 16;
-      const uint8_t* const trx = tb + lr * kBlock + (((2 * kg) ^ (lr >> 1)) & 7) * 16;
-      const uint8_t* const try_ = tb + lr * kBlock + (((2 * kg + 1) ^ (lr >> 1)) & 7) * 16;
+      uint8_t* const tw0 = tb + wr * kBlock + (wc ^ slot_key8(wr)) * 16;
+      uint8_t* const tw1 = tb + (wr + 8) * kBlock + (wc ^ slot_key8(wr + 8)) * 16;
+      const uint8_t* const trx = tb + lr * kBlock + ((2 * kg) ^ slot_key8(lr)) * 16;
+      const uint8_t* const try_ = tb + lr * kBlock + ((2 * kg + 1) ^ slot_key8(lr)) * 16;
       v4i B0[kDecDepth], B1[kDecDepth];
       auto load = [&](int d, int j) {
         const uint8_t* p = wsrc + (size_t)min(j, n - 1) * kBlock;
@@ -584,7 +585,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     } else if (!two) {
       constexpr int kStepDepth2 = 2;   // (register budget shared with the staged path)
       // carriers: wave q loads rows 4q .. 4q + 3 of C's hi term as whole lines (lane l: row
-      // 4q + l/16, 16-byte chunk l%16) and publishes them chunk-major; wave 0's lanes < 16 the
+      // 4q + l/16, 16-byte chunk l%16) and publishes them to the stage; wave 0's lanes < 16 the
       // scale of row lane (all lanes load it: no loads under a branch)
       const int ar = 4 * wave + (lane >> 4);
       const _Float16* asrc = ch.hi + (size_t)(row0 + (ar < M ? ar : 0)) * I + (size_t)kb0 * kBlock + (lane & 15) * 8;
@@ -601,12 +602,16 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       };
       auto step = [&](int d, int j) {
         G2Stage& st = ring[j & 1];
-        *reinterpret_cast<v4i*>(st.a + ((lane & 15) * 16 + ar) * 8) = AR[d];
+        *reinterpret_cast<v4i*>(st.a + ar * (2 * kBlock) + ((lane & 15) ^ slot_key16(ar)) * 16) = AR[d];
         if (wave == 0 && lane < 16) st.sa[lane] = SR[d];
         __syncthreads();
+        // chunk 4 kg + t sits at byte (4 kg ^ key) * 16 ^ 16 t of the row: one base register,
+        // formed here (hoisted, the four addresses stay live across the loop and spill)
+        int rb = lr * (2 * kBlock) + ((4 * kg) ^ slot_key16(lr)) * 16;
+        asm volatile("" : "+v"(rb));
         v8h ah[4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) ah[t] = *reinterpret_cast<const v8h*>(st.a + ((4 * kg + t) * 16 + lr) * 8);
+        for (int t = 0; t < 4; t++) ah[t] = *reinterpret_cast<const v8h*>(st.a + (rb ^ (16 * t)));
         const float4 sa = *reinterpret_cast<const float4*>(st.sa + 4 * kg);
         const float sw = readlane_f32(swv, j);
         v8h b16[4];

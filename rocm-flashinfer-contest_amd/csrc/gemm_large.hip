@@ -423,7 +423,7 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm1_large_kernel(Problem pb, 
 // schedules the reads with exact lgkmcnt waits and never drains the DMAs before them.
 //
 // LDS stage: A [128 rows][128 B], B [256 rows][128 B], 128 row scales.  A row's 16-byte chunk c
-// sits in slot c ^ key(row), key(row) = (row & 7) ^ ((row >> 3) & 1): a DMA instruction writes 8
+// sits in slot c ^ slot_key8(row): a DMA instruction writes 8
 // rows x 8 slots in lane order (each lane fetching the chunk that belongs in its slot, 8 lanes
 // per 128-byte row segment), and an MFMA operand read (16 rows, two chunks per lane) puts any 16
 // consecutive lanes on distinct 16-byte bank groups of a 256-byte bank row (and any 8 on distinct
@@ -437,8 +437,6 @@ constexpr int kBgA = kBgRows * 128;
 constexpr int kBgB = kBgWRows * 128;
 constexpr int kBgStage = kBgA + kBgB + kBgRows * 4;
 constexpr int kBgOps = 2 + 4 + 1;            // per wavefront and K-block: A, B and row-scale DMAs
-
-__device__ __forceinline__ int bg_key(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
 // LDS row R of a 128-row unit -> row of the permuted pairs.  Regular blocks: R < rows.  A mixed
 // block (an expert's last regular block with its <= 32 exact-product rows folded in) puts its
@@ -492,8 +490,8 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
   // DMA lane roles: row (lane / 8) of an 8-row group, slot lane % 8
   const int drow = lane >> 3, dslot = lane & 7;
   // operand read offsets inside a 16-row tile (swizzled chunks 2kg and 2kg + 1 of row lr)
-  const int rd0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
-  const int rd1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
+  const int rd0 = lr * 128 + (((2 * kg) ^ slot_key8(lr)) * 16);
+  const int rd1 = lr * 128 + (((2 * kg + 1) ^ slot_key8(lr)) * 16);
   // DMA sources as per-lane byte offsets from wave-uniform bases: A rows 16w + 8q + drow (the
   // tokens' hidden rows, clamped to the block), B LDS rows 32w + 8q + drow (LDS row R holds n-tile
   // (R % 64) / 16 of weight-row group R / 64: 0, 1 up, 2, 3 gate), row scales of rows 64 (w % 2) + lane
@@ -502,14 +500,14 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
   for (int q = 0; q < 2; q++) {
     const int r = 16 * wave + 8 * q + drow;
     const int tok = pl.perm_token[row0 + min(r, rows - 1)];
-    aoff[q] = (uint32_t)tok * (uint32_t)H + (uint32_t)((dslot ^ bg_key(r)) * 16);
+    aoff[q] = (uint32_t)tok * (uint32_t)H + (uint32_t)((dslot ^ slot_key8(r)) * 16);
   }
 #pragma unroll
   for (int q = 0; q < 4; q++) {
     const int R = 32 * wave + 8 * q + drow;
     const int g = R >> 6, n = (R >> 4) & 3, rr = R & 15;
     const int wrow = (n < 2 ? 0 : I) + cb * kBlock + 32 * g + 16 * (n & 1) + rr;
-    boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ bg_key(R)) * 16);
+    boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ slot_key8(R)) * 16);
   }
   const uint32_t soff = 4u * (uint32_t)pl.perm_token[row0 + min(64 * (wave & 1) + lane, rows - 1)];
   const uint8_t* wbase = pb.w13 + (size_t)e * 2 * I * H;
@@ -644,8 +642,8 @@ __device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Pl
   // DMA lane roles: row (lane / 8) of an 8-row group, slot lane % 8
   const int drow = lane >> 3, dslot = lane & 7;
   // operand read offsets inside a 16-row tile (swizzled chunks 2kg and 2kg + 1 of row lr)
-  const int rd0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
-  const int rd1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
+  const int rd0 = lr * 128 + (((2 * kg) ^ slot_key8(lr)) * 16);
+  const int rd1 = lr * 128 + (((2 * kg + 1) ^ slot_key8(lr)) * 16);
   // DMA sources as per-lane byte offsets from wave-uniform bases: A rows 16w + 8q + drow (the
   // tokens' hidden rows), B LDS rows 32w + 8q + drow (LDS row R holds n-tile (R % 64) / 16 of
   // weight-row group R / 64: 0, 1 up, 2, 3 gate), row scales of rows 64 (w % 2) + lane
@@ -654,14 +652,14 @@ __device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Pl
   for (int q = 0; q < 2; q++) {
     const int r = 16 * wave + 8 * q + drow;
     const int tok = pl.perm_token[rm.src(r)];
-    aoff[q] = (uint32_t)tok * (uint32_t)H + (uint32_t)((dslot ^ bg_key(r)) * 16);
+    aoff[q] = (uint32_t)tok * (uint32_t)H + (uint32_t)((dslot ^ slot_key8(r)) * 16);
   }
 #pragma unroll
   for (int q = 0; q < 4; q++) {
     const int R = 32 * wave + 8 * q + drow;
     const int g = R >> 6, n = (R >> 4) & 3, rr = R & 15;
     const int wrow = (n < 2 ? 0 : I) + cb * kBlock + 32 * g + 16 * (n & 1) + rr;
-    boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ bg_key(R)) * 16);
+    boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ slot_key8(R)) * 16);
   }
   const uint32_t soff = 4u * (uint32_t)pl.perm_token[rm.src(64 * (wave & 1) + lane)];
   const uint8_t* wbase = pb.w13 + (size_t)e * 2 * I * H;
@@ -1045,7 +1043,7 @@ __global__ __launch_bounds__(kLgThreads, 2) void gemm2_large_kernel(Problem pb, 
 // two 32-K MFMAs t = 0, 1 (the same order for both operands): its W2 bytes are one 16-byte
 // chunk, its hi (and lo) values two.
 //
-// LDS stage: hi [128 rows][128 B] and lo [128 rows][128 B] (chunks swizzled by bg_key), W2
+// LDS stage: hi [128 rows][128 B] and lo [128 rows][128 B] (chunks swizzled by slot_key8), W2
 // [256 rows][64 B] (chunk c of row r in slot c ^ bg_key4(r)), 128 row scales of C.
 constexpr int kB2Cols = 256;
 constexpr int kB2Hi = kBgRows * 128;
@@ -1054,9 +1052,12 @@ constexpr int kB2W = kB2Cols * 64;
 constexpr int kB2Stage = kB2Hi + kB2Lo + kB2W + kBgRows * 4;
 constexpr int kB2Stages = 3;
 
-// 4-slot swizzle of 64-byte rows: any 16 consecutive rows reading one chunk hit distinct 16-byte
-// bank groups of a 256-byte bank row, and any 8 (same row parity) of a 128-byte one.
-__device__ __forceinline__ int bg_key4(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
+// 4-slot swizzle of 64-byte rows: chunk c of row r sits in slot c ^ key(r), key linear in the row
+// bits 1, 2, 3 (weights 1, 2, 3).  An MFMA operand read has lanes (row r = 0..15, chunk kg), and the
+// slots are conflict-free whether the LDS serves a 16-byte read 8, 16 or 32 lanes at a time (over
+// 128, 256 or 512 bytes of banks): 8 rows of one parity, 16 consecutive rows and rows r, r + 8 with
+// kg, kg ^ 1 all land on distinct 16-byte bank groups.
+__device__ __forceinline__ int bg_key4(int row) { return ((row >> 1) & 3) ^ (((row >> 3) & 1) * 3); }
 
 // e4m3 x 16 -> two f16 x 8 (MFMA operand order k = 8t + 0..7), exactly
 __device__ __forceinline__ void widen16(const v4i& x, v8h& t0, v8h& t1) {
@@ -1092,7 +1093,7 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
 #pragma unroll
   for (int q = 0; q < 2; q++) {
     const int r = 16 * wave + 8 * q + (lane >> 3);
-    hoff[q] = (uint32_t)rm.src(r) * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ bg_key(r))) * 16);
+    hoff[q] = (uint32_t)rm.src(r) * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ slot_key8(r))) * 16);
   }
 #pragma unroll
   for (int q = 0; q < 2; q++) {
@@ -1117,9 +1118,9 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
       dma_lds16_s(woff[q], wbase + (size_t)k * 64, st + kB2Hi + kB2Lo + (32 * wave + 16 * q) * 64);
     dma_lds4_s(soff, ch.scale + k / 2, st + kB2Hi + kB2Lo + kB2W + (wave & 1) * 256);
   };
-  // operand read offsets: hi / lo chunks 2kg + t of row lr (bg_key), W2 chunk kg of row lr (bg_key4)
-  const int rh0 = lr * 128 + (((2 * kg) ^ bg_key(lr)) * 16);
-  const int rh1 = lr * 128 + (((2 * kg + 1) ^ bg_key(lr)) * 16);
+  // operand read offsets: hi / lo chunks 2kg + t of row lr (slot_key8), W2 chunk kg of row lr (bg_key4)
+  const int rh0 = lr * 128 + (((2 * kg) ^ slot_key8(lr)) * 16);
+  const int rh1 = lr * 128 + (((2 * kg + 1) ^ slot_key8(lr)) * 16);
   const int rq = lr * 64 + ((kg ^ bg_key4(lr)) * 16);
 
   MOEFP8_WAIT_VMCNT(0);

@@ -114,6 +114,15 @@ __device__ __forceinline__ bool needs_exact_products(float a2, float w, float s1
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
+// LDS slot swizzles of 16-byte chunks: chunk c of row r sits in slot c ^ key(r).  The keys are
+// linear in the row bits and were chosen so that the MFMA operand reads (lanes = 16 rows x chunk
+// groups) and the row-order writes of the stages below are conflict-free whether the LDS serves
+// a 16-byte access 8, 16 or 32 lanes at a time (over 128, 256 or 512 bytes of banks).
+// 128-byte rows (8 slots):
+__device__ __forceinline__ int slot_key8(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+// 256-byte rows (16 slots):
+__device__ __forceinline__ int slot_key16(int row) { return (row & 11) ^ (((row >> 2) & 1) * 5); }
+
 // A value the caller knows to be equal on every lane, moved to a scalar register.
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 // Wavefront index inside the workgroup, as a wave-uniform (scalar) value.

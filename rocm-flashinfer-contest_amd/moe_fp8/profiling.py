@@ -34,6 +34,7 @@ except ImportError:  # run as a script
 
 FIRST_KERNEL = "route_kernel"     # every operator call starts with the routing kernel
 MI355X_CUS = 256
+MI355X_XCDS = 8           # GRBM_GUI_ACTIVE reads the sum over the XCDs
 SIMDS_PER_CU = 4
 
 
@@ -140,8 +141,9 @@ def counter_means(dirs):
 
 def derived(c):
     """Ratios from one kernel's counters (None where a counter is missing):
-    mfma_busy   = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x CUs x 4 SIMDs), the fraction of
-                  SIMD-cycles the matrix cores were busy while the GPU was;
+    mfma_busy   = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCDs x CUs x 4 SIMDs), the fraction
+                  of SIMD-cycles the matrix cores were busy while the GPU was (GRBM_GUI_ACTIVE is
+                  summed over the XCDs, SQ_VALU_MFMA_BUSY_CYCLES over the SIMDs);
     lds_conflict = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE, the share of LDS-active cycles lost
                   to bank conflicts;
     valu_per_mfma = SQ_INSTS_VALU / SQ_INSTS_MFMA (the MFMA instructions are counted in both)."""
@@ -149,7 +151,7 @@ def derived(c):
         return c.get(n)
     out = {}
     if g("SQ_VALU_MFMA_BUSY_CYCLES") is not None and g("GRBM_GUI_ACTIVE"):
-        out["mfma_busy"] = g("SQ_VALU_MFMA_BUSY_CYCLES") / (g("GRBM_GUI_ACTIVE") * MI355X_CUS * SIMDS_PER_CU)
+        out["mfma_busy"] = g("SQ_VALU_MFMA_BUSY_CYCLES") / (g("GRBM_GUI_ACTIVE") / MI355X_XCDS * MI355X_CUS * SIMDS_PER_CU)
     if g("SQ_LDS_BANK_CONFLICT") is not None and g("SQ_LDS_IDX_ACTIVE"):
         out["lds_conflict"] = g("SQ_LDS_BANK_CONFLICT") / g("SQ_LDS_IDX_ACTIVE")
     if g("SQ_INSTS_VALU") is not None and g("SQ_INSTS_MFMA"):
