@@ -7,8 +7,9 @@ kernel-source hash (``build.source_hash()``), so ``bench.py`` can tell a record 
 current kernels from a stale one.
 
     python -m moe_fp8.profiling trace    <rocprof-dir> --workload W --steps K --warmup N --cmd "..." --out F
-    python -m moe_fp8.profiling counters <rocprof-dir> [<rocprof-dir> ...] --workload W --cmd "..." --out F
-    python -m moe_fp8.profiling traffic  <fetch-dir> <write-dir> --kernel K --workload W --cmd "..." --out F
+    python -m moe_fp8.profiling counters <rocprof-dir> [<rocprof-dir> ...] --workload W --cmd "..." [--cmd ...]
+                                         [--copy-record profiles/traffic_copy.txt] --out F
+    python -m moe_fp8.profiling traffic  <fetch-dir> <write-dir> --kernel K --workload W --cmd "..." --cmd "..." --out F
 
 ``trace`` reads ``*kernel_trace.csv``; ``counters`` and ``traffic`` read
 ``*counter_collection.csv`` (``rocprofv3 --output-format csv``).  The bench command the
@@ -50,8 +51,9 @@ def _csvs(d, suffix):
 
 
 def _stamp_lines(workload, cmd):
-    return [f"source {source_hash()} (kernel-source hash of the library the numbers were taken with)",
-            f"workload {workload}", f"command: cd /tmp && {cmd}"]
+    cmds = [cmd] if isinstance(cmd, str) else list(cmd)
+    return ([f"source {source_hash()} (kernel-source hash of the library the numbers were taken with)",
+             f"workload {workload}"] + [f"command: cd /tmp && {c}" for c in cmds])
 
 
 def trace_calls(d):
@@ -235,12 +237,12 @@ def main(argv=None):
     t.add_argument("--workload", required=True)
     t.add_argument("--steps", type=int, required=True)
     t.add_argument("--warmup", type=int, required=True)
-    t.add_argument("--cmd", required=True)
+    t.add_argument("--cmd", required=True, action="append", help="a command the numbers come from (repeatable)")
     t.add_argument("--out", required=True)
     c = sub.add_parser("counters")
     c.add_argument("dirs", nargs="+")
     c.add_argument("--workload", required=True)
-    c.add_argument("--cmd", required=True)
+    c.add_argument("--cmd", required=True, action="append", help="a command the numbers come from (repeatable)")
     c.add_argument("--out", required=True)
     c.add_argument("--copy-record", default=None, help="traffic_copy.txt, to turn FETCH/WRITE_SIZE into bytes")
     r = sub.add_parser("traffic")
@@ -248,7 +250,7 @@ def main(argv=None):
     r.add_argument("write_dir")
     r.add_argument("--kernel", required=True)
     r.add_argument("--workload", required=True)
-    r.add_argument("--cmd", required=True)
+    r.add_argument("--cmd", required=True, action="append", help="a command the numbers come from (repeatable)")
     r.add_argument("--out", required=True)
     a = ap.parse_args(argv)
     if a.what == "trace":
