@@ -233,7 +233,9 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
       {
         // rows [0, M) x K-blocks [kb0, kb0 + n) in 16-byte chunks (<= 4 per thread), then the
         // M x n scales (<= 128), all loads issued before the first store
-        constexpr int kPer = kPreRows * kPreMaxKB * (kBlock / 16) / (64 * kDecBlockWaves);
+        constexpr int kChunks = kPreRows * kPreMaxKB * (kBlock / 16);
+        constexpr int kPer = (kChunks + 64 * kDecBlockWaves - 1) / (64 * kDecBlockWaves);
+        static_assert(kPer * 64 * kDecBlockWaves >= kChunks, "every staged chunk has a thread");
         const int nch = M * n * (kBlock / 16);
         v4i v[kPer];
 #pragma unroll
@@ -529,7 +531,9 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
         // rows [0, M) x K-blocks [kb0, kb0 + n) of C's hi term in 16-byte chunks (<= 4 per
         // thread), then the M x n scales, all loads issued before the first store
         constexpr int kChunksPerKB = kBlock * 2 / 16;
-        constexpr int kPer = kPreRows * kPre2MaxKB * kChunksPerKB / (64 * kDecBlockWaves);
+        constexpr int kChunks = kPreRows * kPre2MaxKB * kChunksPerKB;
+        constexpr int kPer = (kChunks + 64 * kDecBlockWaves - 1) / (64 * kDecBlockWaves);
+        static_assert(kPer * 64 * kDecBlockWaves >= kChunks, "every staged chunk has a thread");
         const int nch = M * n * kChunksPerKB;
         v4i v[kPer];
 #pragma unroll

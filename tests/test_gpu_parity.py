@@ -353,3 +353,25 @@ def test_full_path_workloads(name, full_weights):
         assert counts.min() == 0 and counts.max() > 2000
     if name.endswith("_local"):          # the full-size weight-streaming GEMMs with 1-4 rows ran
         assert int(counts.sum()) >= 1 and float(ref32.abs().max()) > 0.0
+
+
+def test_full_path_four_row_tile_on_two_way_split(full_weights):
+    """A decode call whose GEMM1 splits K in two (28 K-blocks per unit at H=7168: 6 to 10 m-tiles)
+    with an expert of exactly 4 tokens: the staged path's largest case (4 rows x 28 K-blocks,
+    every staging thread busy).  Local expert 5 is forced onto tokens 0-3 and kept off the others."""
+    wl = WORKLOADS["decode_t16"]
+    w_dev, w_cpu = full_weights
+    logits, bias, hs, hss = W.make_activations(wl, device=DEV)
+    logits = logits.clone()
+    logits[:4, 5] += 8.0
+    logits[4:, 5] -= 8.0
+    act = (logits, bias, hs, hss)
+    act_cpu = to_cpu(act)
+    ridx, rw, _, _ = oracle_route(act_cpu[0], act_cpu[1])
+    counts, _, _, _ = O.permute(ridx, rw, 32, 0)
+    n_mt = int(sum((c + 15) // 16 for c in counts))
+    assert counts[5] == 4 and 6 <= n_mt <= 10, (counts.tolist(), n_mt)
+    out = moe_fp8.run(*act, *w_dev, 0, W.RSF)
+    torch.cuda.synchronize()
+    ref32, _ = O.moe_forward(*act_cpu, *w_cpu, 0, W.RSF)
+    assert_close(out, ref32, "four-row tile, two-way split")
