@@ -25,6 +25,8 @@
 //        to f16 (exact products, 2^-11 relative input error); m-blocks flagged by GEMM1 add
 //        the lo term on the f16 MFMA.  Rows are scaled by the routing weight (main.py:240)
 //        and summed per token by the combine kernel.
+#include <type_traits>
+
 #include "moefp8_device.h"
 #include "moefp8_launch.h"
 
@@ -1130,7 +1132,11 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
   for (int i = 0; i < NT; i++)
 #pragma unroll
     for (int n = 0; n < 4; n++) acc[i][n] = v4f{0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < KS; j++) {
+  // The two 64-K stages of a 128-K scale block chain their MFMAs into one product per tile
+  // (pp), scaled into acc once per block: half the scale FMAs and products of a stage each.
+  v4f pp[NT][4];
+  auto stage = [&](int j, auto first_c) {
+    constexpr bool kFirst = decltype(first_c)::value;
     // one stage in flight past the current one: kOps operations per wavefront
     static_assert(kB2Stages == 3, "wait count");
     if constexpr (kOps == 5) MOEFP8_WAIT_VMCNT(5);
@@ -1153,23 +1159,35 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
         l0 = as_v8h(*reinterpret_cast<const v4i*>(ht + kB2Hi + rh0));
         l1 = as_v8h(*reinterpret_cast<const v4i*>(ht + kB2Hi + rh1));
       }
-      const float4 sa = *reinterpret_cast<const float4*>(st + kB2Hi + kB2Lo + kB2W + (16 * t + 4 * kg) * 4);
-      const float4 sc = {sa.x * sw, sa.y * sw, sa.z * sw, sa.w * sw};
 #pragma unroll
       for (int n = 0; n < 4; n++) {
-        v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b16[n][0], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        v4f p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b16[n][0], kFirst ? v4f{0.f, 0.f, 0.f, 0.f} : pp[i][n],
+                                                       0, 0, 0);
         p = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b16[n][1], p, 0, 0, 0);
         if constexpr (kTwo) {
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l0, b16[n][0], p, 0, 0, 0);
           p = __builtin_amdgcn_mfma_f32_16x16x32_f16(l1, b16[n][1], p, 0, 0, 0);
         }
-        acc[i][n][0] += p[0] * sc.x;
-        acc[i][n][1] += p[1] * sc.y;
-        acc[i][n][2] += p[2] * sc.z;
-        acc[i][n][3] += p[3] * sc.w;
+        pp[i][n] = p;
+      }
+      if constexpr (!kFirst) {
+        const float4 sa = *reinterpret_cast<const float4*>(st + kB2Hi + kB2Lo + kB2W + (16 * t + 4 * kg) * 4);
+        const float4 sc = {sa.x * sw, sa.y * sw, sa.z * sw, sa.w * sw};
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+          acc[i][n][0] += pp[i][n][0] * sc.x;
+          acc[i][n][1] += pp[i][n][1] * sc.y;
+          acc[i][n][2] += pp[i][n][2] * sc.z;
+          acc[i][n][3] += pp[i][n][3] * sc.w;
+        }
       }
     }
     issue(j + kB2Stages - 1);
+  };
+  // KS = I / 64 is even (I is a multiple of 128)
+  for (int j = 0; j < KS; j += 2) {
+    stage(j, std::true_type{});
+    stage(j + 1, std::false_type{});
   }
   MOEFP8_WAIT_VMCNT(0);
   // the workgroup's next unit, claimed now so that the atomic overlaps the epilogue
