@@ -115,6 +115,8 @@ REDUCED = [
     (100, 4, 256, 128, -2),
     (50, 32, 256, 128, 300),
     (2500, 32, 256, 128, 0),
+    (2048, 32, 256, 128, 0),        # one-workgroup permutation, two rounds of 4 token blocks
+    (1100, 32, 256, 128, 0),        # ... and a second round with one block
     (2100, 16, 512, 256, 0),        # 128-row blocks with 4 K-blocks
     (16, 32, 512, 256, 32),         # expert-parallel rank 1 (one routing group)
     (40, 32, 256, 128, 240),        # rank owning experts 240..271: half past the last expert
