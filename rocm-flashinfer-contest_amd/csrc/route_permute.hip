@@ -231,24 +231,35 @@ __device__ void route_token(const float (&x)[4], const float (&b)[4], float rsf,
   }
 }
 
-// One leading block per local expert for the weight-scale estimates (first, so that they run
-// beside the token blocks instead of after them), then one wavefront per token
-// (kSigmaThreads / 64 tokens per block).
+// Blocks in order: one per local expert for the weight-scale estimates, then, with the magnitude
+// inputs, the hidden-row norm blocks, then the routing blocks (the two leading kinds first, so
+// that they run beside the routing blocks instead of after them).  Norm and routing blocks take
+// one token per wavefront (kSigmaThreads / 64 tokens per block): the norm streams the hidden
+// rows while the routing arithmetic runs on other wavefronts.
 __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __restrict__ logits, int logits_dt,
                                                               const void* __restrict__ bias, int bias_dt, int64_t T,
                                                               float rsf, int* __restrict__ topk_ids,
                                                               float* __restrict__ topk_w, int token_blocks,
-                                                              MagArgs mg, int* __restrict__ zero, int n_zero) {
-  const int sigma_blocks = (int)gridDim.x - token_blocks;
+                                                              int norm_blocks, MagArgs mg, int* __restrict__ zero,
+                                                              int n_zero) {
+  const int sigma_blocks = (int)gridDim.x - token_blocks - norm_blocks;
+  const int lane = lane_id();
+  const int wave = threadIdx.x >> 6;
+  constexpr int kWavesPerBlock = kSigmaThreads / kWave;
   if ((int)blockIdx.x < sigma_blocks) {
     expert_sigma_block(mg, blockIdx.x);
     return;
   }
-  const int tb = (int)blockIdx.x - sigma_blocks;   // token block
+  if ((int)blockIdx.x < sigma_blocks + norm_blocks) {
+    const int nb = (int)blockIdx.x - sigma_blocks;
+    for (int64_t t = (int64_t)nb * kWavesPerBlock + wave; t < T; t += (int64_t)norm_blocks * kWavesPerBlock) {
+      const float a2 = token_sq_norm(mg.hidden, mg.hscale, mg.H, T, t);
+      if (lane == 0) mg.tok_a2[t] = a2;
+    }
+    return;
+  }
+  const int tb = (int)blockIdx.x - sigma_blocks - norm_blocks;   // routing block
   for (int i = tb * kSigmaThreads + threadIdx.x; i < n_zero; i += token_blocks * kSigmaThreads) zero[i] = 0;
-  const int lane = lane_id();
-  const int wave = threadIdx.x >> 6;
-  constexpr int kWavesPerBlock = kSigmaThreads / kWave;
   float b[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) b[i] = load_as_f32(bias, bias_dt, 4 * lane + i);
@@ -256,11 +267,7 @@ __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __rest
   for (int64_t t = (int64_t)tb * kWavesPerBlock + wave; t < T;
        t += (int64_t)token_blocks * kWavesPerBlock) {
     float x[4];
-    load_logits(logits, logits_dt, t, x);       // issued before the hidden-row loads
-    if (mg.hidden) {
-      const float a2 = token_sq_norm(mg.hidden, mg.hscale, mg.H, T, t);
-      if (lane == 0) mg.tok_a2[t] = a2;
-    }
+    load_logits(logits, logits_dt, t, x);
     int id;
     float w;
     route_token(x, b, rsf, &id, &w);
@@ -291,8 +298,12 @@ void launch_route(const void* logits, int logits_dt, const void* bias, int bias_
     mg.esig = mag->esig;
     extra = mag->E_local;
   }
-  hipLaunchKernelGGL(route_kernel, dim3((unsigned)(blocks + extra)), dim3(kSigmaThreads), 0, stream, logits, logits_dt,
-                     bias, bias_dt, T, rsf, topk_ids, topk_w, (int)blocks, mg, zero, n_zero);
+  // the norm blocks stream the hidden rows (bandwidth-bound): 256 of them (each wavefront then
+  // takes T / 1024 rows in turn) leave the CUs' slots to the routing blocks at large T
+  const int norm_blocks = mag ? (int)(blocks < 256 ? blocks : 256) : 0;
+  hipLaunchKernelGGL(route_kernel, dim3((unsigned)(blocks + norm_blocks + extra)), dim3(kSigmaThreads), 0, stream,
+                     logits, logits_dt, bias, bias_dt, T, rsf, topk_ids, topk_w, (int)blocks, norm_blocks, mg, zero,
+                     n_zero);
 }
 
 
