@@ -116,16 +116,26 @@ __device__ float token_sq_norm(const uint8_t* hidden, const float* hscale, int H
   return wave_sum_f32(a2);
 }
 
+// Elements [i, i + 4) of a tensor of dtype dt (0 f32, 1 bf16, 2 f16; i a multiple of 4, the
+// tensor 16-byte aligned) as fp32: two 8-byte loads (a 16-bit type loads its 8 bytes twice) and
+// selects instead of branches, so that the loads of the bias and of a token's logits leave
+// together (a load under a dtype branch is waited for before the next one is issued).
+__device__ __forceinline__ void load4_as_f32(const void* p, int dt, int64_t i, float (&x)[4]) {
+  const uint8_t* b = reinterpret_cast<const uint8_t*>(p) + i * (dt == 0 ? 4 : 2);
+  const uint2 u = *reinterpret_cast<const uint2*>(b);
+  const uint2 v = *reinterpret_cast<const uint2*>(b + (dt == 0 ? 8 : 0));
+  const uint32_t w[4] = {u.x, u.y, v.x, v.y};
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const uint16_t h = (uint16_t)((k & 1) ? (w[k >> 1] >> 16) : (w[k >> 1] & 0xffffu));
+    const float f16v = dt == 1 ? bf16_to_f32(h) : half_to_f32(h);
+    x[k] = dt == 0 ? __uint_as_float(w[k]) : f16v;
+  }
+}
+
 // The 4 logits of lane l (experts 4l..4l+3) of token t, as fp32.
 __device__ __forceinline__ void load_logits(const void* logits, int logits_dt, int64_t t, float (&x)[4]) {
-  const int lane = lane_id();
-  if (logits_dt == 0) {
-    const float4 v = reinterpret_cast<const float4*>(logits)[t * (kEGlobal / 4) + lane];
-    x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; i++) x[i] = load_as_f32(logits, logits_dt, t * kEGlobal + 4 * lane + i);
-  }
+  load4_as_f32(logits, logits_dt, t * kEGlobal + 4 * lane_id(), x);
 }
 
 // Merge of two (largest, second largest) pairs.
@@ -260,17 +270,17 @@ __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __rest
   }
   const int tb = (int)blockIdx.x - sigma_blocks - norm_blocks;   // routing block
   for (int i = tb * kSigmaThreads + threadIdx.x; i < n_zero; i += token_blocks * kSigmaThreads) zero[i] = 0;
-  float b[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) b[i] = load_as_f32(bias, bias_dt, 4 * lane + i);
-
-  for (int64_t t = (int64_t)tb * kWavesPerBlock + wave; t < T;
-       t += (int64_t)token_blocks * kWavesPerBlock) {
-    float x[4];
-    load_logits(logits, logits_dt, t, x);
+  // the first token's logits (a clamped row: no branch) leave with the bias, one round trip
+  // for both; each later token's logits are loaded while the current one is routed
+  const int64_t t0 = (int64_t)tb * kWavesPerBlock + wave, stride = (int64_t)token_blocks * kWavesPerBlock;
+  float x[4], b[4];
+  load_logits(logits, logits_dt, t0 < T ? t0 : T - 1, x);
+  load4_as_f32(bias, bias_dt, 4 * lane, b);
+  for (int64_t t = t0; t < T; t += stride) {
     int id;
     float w;
     route_token(x, b, rsf, &id, &w);
+    if (t + stride < T) load_logits(logits, logits_dt, t + stride, x);
     if (lane < kTopK) {
       topk_ids[t * kTopK + lane] = id;
       topk_w[t * kTopK + lane] = w;
