@@ -16,6 +16,7 @@ constexpr int kSmallT = 64;
 constexpr int kSmallTile = 16;
 constexpr int kSmallPairs = kSmallT * kTopK;
 constexpr int kSmallMaxMtiles = kSmallPairs / kSmallTile + kEGlobal;
+constexpr int kPlanThreads = 256;   // threads of a workgroup that builds the plan
 
 // What the GEMM reads while it runs ...
 struct DecodePlanLds {
@@ -44,23 +45,42 @@ __device__ __forceinline__ int pick_split(int n_mt, int ncb, int kb, int slots, 
   return s_min;
 }
 
-// Builds the plan in `L` using `X` (every thread of the workgroup takes part; ends with a
-// barrier).
+// Builds the plan in `L` using `X` (every thread of a workgroup of kPlanThreads takes part;
+// ends with a barrier).
 // With `global`, also writes expert_offsets, active, mtile_offsets, info {P, active experts,
 // m-tiles, S1, S2}, perm_token, perm_w, tok_slot (each token's pair rows in ascending local
 // expert order, -1 past its last) and the m-tile table.
 __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, DecodePlanScratch& X, bool global) {
   const int tid = threadIdx.x, nth = blockDim.x, lane = lane_id(), wave = tid >> 6;
   const int T = a.T, E = a.E_local, NP = T * kTopK;
-  // every global input in one round of loads: ids, weights, token norms, expert estimates
-  for (int e = tid; e < E; e += nth) X.tmask[e] = 0ull;
-  for (int i = tid; i < 2 * E; i += nth) X.esig[i] = a.esig[i];
-  for (int t = tid; t < T; t += nth) X.a2[t] = a.tok_a2[t];
-  for (int i = tid; i < NP; i += nth) {
-    const int le = a.topk_ids[i] - a.offset;
-    X.ids[i] = le >= 0 && le < E ? le : -1;
-    X.w[i] = a.topk_w[i];
+  // every global input in one round of loads: each thread loads its (at most two) ids and
+  // weights, one token norm and its (at most two) expert estimates at clamped indices, with no
+  // branch between the loads (loads in bounded loops were each waited for before the next loop's),
+  // then stores those in range
+  static_assert(2 * kPlanThreads >= kSmallPairs && 2 * kPlanThreads >= 2 * kEGlobal && kPlanThreads >= kSmallT,
+                "two loads per thread cover every input");
+  int idv[2];
+  float wv[2], ev[2];
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int i = min(tid + q * kPlanThreads, NP - 1), k = min(tid + q * kPlanThreads, 2 * E - 1);
+    idv[q] = a.topk_ids[i];
+    wv[q] = a.topk_w[i];
+    ev[q] = a.esig[k];
   }
+  const float av = a.tok_a2[min(tid, T - 1)];
+  for (int e = tid; e < E; e += nth) X.tmask[e] = 0ull;
+#pragma unroll
+  for (int q = 0; q < 2; q++) {
+    const int i = tid + q * kPlanThreads;
+    if (i < NP) {
+      const int le = idv[q] - a.offset;
+      X.ids[i] = le >= 0 && le < E ? le : -1;
+      X.w[i] = wv[q];
+    }
+    if (i < 2 * E) X.esig[i] = ev[q];
+  }
+  if (tid < T) X.a2[tid] = av;
   __syncthreads();
   for (int i = tid; i < NP; i += nth)
     if (X.ids[i] >= 0) atomicOr(&X.tmask[X.ids[i]], 1ull << (i >> 3));

@@ -38,6 +38,7 @@ constexpr int kDec2BlocksPerCU = 5;          // GEMM2 too (<= 96 VGPRs: its per-
                                              // shallower ring; a scratch spill there cost ~20% of
                                              // the kernel's time, measured)
 constexpr int kDecDepth = 3;                 // K-blocks in flight per wavefront (register ring)
+static_assert(64 * kDecBlockWaves == kPlanThreads, "the GEMM1 workgroups build the plan");
 
 __device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
   const v4i* q = reinterpret_cast<const v4i*>(p);
@@ -498,10 +499,12 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     asm volatile("" : "+v"(lane));
     const int lr = lane & 15, kg = lane >> 4;
     const DecUnit du = decode_unit(u, S, NCB);
+    // the m-tile and GEMM1's measured flag loaded together (not the flag behind the tile's test)
+    const int measured = pl.two_term[du.g];
     const int4 mt = pl.mtiles[du.g];
     const int e = uniform(mt.x), row0 = uniform(mt.y), M = uniform(mt.z);
     // both f16 terms of C: predicted (the plan), or measured by GEMM1
-    const bool two = (uniform(mt.w) & kFlagTwoTermC) || uniform(pl.two_term[du.g]) != 0;
+    const bool two = ((uniform(mt.w) & kFlagTwoTermC) | uniform(measured)) != 0;
     const int kb0 = du.s * KB / S, n = (du.s + 1) * KB / S - kb0;
     const int cg = du.cb * kDecBlockWaves + wave;
     const uint8_t* bp = pb.w2 + ((size_t)e * H + cg * 16 + lr) * I + (size_t)kb0 * kBlock + kg * 32;
