@@ -62,7 +62,7 @@ def test_route_bit_exact_on_workloads(name):
 
 
 @pytest.mark.parametrize("bias_dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("logits_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("logits_dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_route_input_dtypes(logits_dtype, bias_dtype):
     print(f"[route dtypes] {logits_dtype} {bias_dtype}", flush=True)
     g = torch.Generator().manual_seed(31)
