@@ -1261,17 +1261,31 @@ __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2
 // of its own between the GEMMs: the same test inside GEMM1's epilogue made the compiler schedule
 // GEMM1's K loop worse.
 __global__ __launch_bounds__(256) void c_flags_kernel(Plan pl, CHalf8 ch, int I) {
+  constexpr int kBatch = 8;   // scales per thread loaded together (a 128-row block at I = 2048: all)
   const int g = blockIdx.x;
-  if (g >= pl.info[2]) return;
+  // the block count and the block (the table holds the launch's grid of entries) in one round of
+  // loads, then the block's scales, routing weights and W2 estimate in another
+  const int n_blocks = pl.info[2];
   const int4 blk = pl.mblocks[g];
+  if (g >= n_blocks) return;
   // a mixed block's exact rows follow its regular rows
   const int n = blk.z + ((blk.w & kFlagMixed) ? (blk.w >> kMixedShift) : 0);
-  const int NCB = I / kBlock;
-  const float sigma2 = pl.esig[2 * blk.x + 1], sqrt_i = sqrtf((float)I);
+  const int NCB = I / kBlock, total = n * NCB;
+  const float sqrt_i = sqrtf((float)I);
   bool need = (blk.w & kFlagTwoTermC) != 0;
-  for (int i = threadIdx.x; i < n * NCB; i += blockDim.x) {
-    const int p = blk.y + i / NCB;
-    need |= needs_two_terms(pl.perm_w[p], sigma2, 448.0f * ch.scale[(size_t)p * NCB + i % NCB], sqrt_i);
+  for (int i0 = 0; i0 < total; i0 += kBatch * (int)blockDim.x) {
+    float sc[kBatch], w[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; q++) {
+      const int i = min(i0 + q * (int)blockDim.x + (int)threadIdx.x, total - 1);
+      const int p = blk.y + i / NCB;
+      sc[q] = ch.scale[(size_t)p * NCB + i % NCB];
+      w[q] = pl.perm_w[p];
+    }
+    const float sigma2 = pl.esig[2 * blk.x + 1];
+#pragma unroll
+    for (int q = 0; q < kBatch; q++)
+      need |= i0 + q * (int)blockDim.x + (int)threadIdx.x < total && needs_two_terms(w[q], sigma2, 448.0f * sc[q], sqrt_i);
   }
   need = __syncthreads_or(need);
   if (threadIdx.x == 0) pl.two_term[g] = need ? 1 : 0;

@@ -42,30 +42,63 @@ __device__ __forceinline__ bool folds_exact(const LargePermArgs& a, int n01, int
   return last <= a.rows_a - 16 * ((n2 + 15) / 16);
 }
 
-// Bucket of slot k of token t, or -1 if the expert is not local.
-__device__ __forceinline__ int pair_bucket(const LargePermArgs& a, int t, int k, float a2, float* w_out, int* le_out) {
-  const int le = a.topk_ids[(size_t)t * kTopK + k] - a.offset;
-  if (le < 0 || le >= a.E_local) return -1;
-  const float w = a.topk_w[(size_t)t * kTopK + k];
-  const float pred = predicted_output_rms(a2, w, a.esig[2 * le], a.esig[2 * le + 1], a.sqrt_i);
-  *w_out = w;
-  *le_out = le;
+// A token's 8 slots (local expert or -1, routing weight) and squared norm, and one thread's share
+// of the experts' estimates for the workgroup's LDS copy: every global input of the permutation's
+// per-token kernels in one round of loads (16-byte loads, clamped indices, no branch between them;
+// loads under a per-slot branch were each waited for before the next).
+struct TokenSlots {
+  int le[kTopK];
+  float w[kTopK];
+  float a2;
+  float es[2];   // esig[tid], esig[tid + kBlkTokens] (clamped)
+};
+__device__ __forceinline__ void load_token_slots(const LargePermArgs& a, int t, TokenSlots& ts) {
+  static_assert(2 * kBlkTokens >= 2 * kEGlobal, "two estimates per thread cover every expert");
+  const int tc = min(t, a.T - 1), tid = threadIdx.x, ne = 2 * a.E_local;
+  const int4* ip = reinterpret_cast<const int4*>(a.topk_ids + (size_t)tc * kTopK);
+  const float4* wp = reinterpret_cast<const float4*>(a.topk_w + (size_t)tc * kTopK);
+  const int4 i0 = ip[0], i1 = ip[1];
+  const float4 w0 = wp[0], w1 = wp[1];
+  ts.a2 = a.tok_a2[tc];
+  ts.es[0] = a.esig[min(tid, ne - 1)];
+  ts.es[1] = a.esig[min(tid + kBlkTokens, ne - 1)];
+  const int id[kTopK] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
+  const float wv[kTopK] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+  for (int k = 0; k < kTopK; k++) {
+    const int le = id[k] - a.offset;
+    ts.le[k] = le >= 0 && le < a.E_local ? le : -1;
+    ts.w[k] = wv[k];
+  }
+}
+// The workgroup's LDS copy of the expert estimates (the caller's barrier publishes it).
+__device__ __forceinline__ void stage_esig(const LargePermArgs& a, const TokenSlots& ts, float* es) {
+  const int tid = threadIdx.x, ne = 2 * a.E_local;
+  if (tid < ne) es[tid] = ts.es[0];
+  if (tid + kBlkTokens < ne) es[tid + kBlkTokens] = ts.es[1];
+}
+// Bucket (local expert x magnitude class) of slot k, or -1 if the expert is not local.
+__device__ __forceinline__ int slot_bucket(const LargePermArgs& a, const TokenSlots& ts, int k, const float* es) {
+  const int le = ts.le[k];
+  if (le < 0) return -1;
+  const float pred = predicted_output_rms(ts.a2, ts.w[k], es[2 * le], es[2 * le + 1], a.sqrt_i);
   return le * kClasses + magnitude_class(pred);
 }
 
 __global__ __launch_bounds__(kBlkTokens) void perm_count_kernel(LargePermArgs a) {
   __shared__ int cnt[kEGlobal * kClasses];
+  __shared__ float es[2 * kEGlobal];
   const int E3 = a.E_local * kClasses, tid = threadIdx.x;
-  for (int i = tid; i < E3; i += kBlkTokens) cnt[i] = 0;
-  __syncthreads();
   const int t = blockIdx.x * kBlkTokens + tid;
+  TokenSlots ts;
+  load_token_slots(a, t, ts);
+  for (int i = tid; i < E3; i += kBlkTokens) cnt[i] = 0;
+  stage_esig(a, ts, es);
+  __syncthreads();
   if (t < a.T) {
-    const float a2 = a.tok_a2[t];
 #pragma unroll
     for (int k = 0; k < kTopK; k++) {
-      float w;
-      int le;
-      const int b = pair_bucket(a, t, k, a2, &w, &le);
+      const int b = slot_bucket(a, ts, k, es);
       if (b >= 0) atomicAdd(&cnt[b], 1);
     }
   }
@@ -231,27 +264,31 @@ __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a)
   // per wavefront and key, the lanes holding it: buckets (expert x class) and experts
   __shared__ unsigned long long bmask[kBlkWaves][kEGlobal * kClasses];
   __shared__ unsigned long long emask[kBlkWaves][kEGlobal];
+  __shared__ float es[2 * kEGlobal];
   const int E = a.E_local, E3 = E * kClasses, tid = threadIdx.x, wave = tid >> 6;
-  for (int i = tid; i < kBlkWaves * E3; i += kBlkTokens) bmask[i / E3][i % E3] = 0ull;
-  for (int i = tid; i < kBlkWaves * E; i += kBlkTokens) emask[i / E][i % E] = 0ull;
-  __syncthreads();
   const int t = blockIdx.x * kBlkTokens + tid;
   const bool in = t < a.T;
+  TokenSlots ts;
+  load_token_slots(a, t, ts);
+  for (int i = tid; i < kBlkWaves * E3; i += kBlkTokens) bmask[i / E3][i % E3] = 0ull;
+  for (int i = tid; i < kBlkWaves * E; i += kBlkTokens) emask[i / E][i % E] = 0ull;
+  stage_esig(a, ts, es);
+  __syncthreads();
   int bk[kTopK], ek[kTopK], rb[kTopK], re[kTopK];
-  float wk[kTopK];
-  const float a2 = in ? a.tok_a2[t] : 0.f;
 #pragma unroll
   for (int k = 0; k < kTopK; k++) {
-    bk[k] = -1;
-    ek[k] = -1;
-    wk[k] = 0.f;
+    bk[k] = in ? slot_bucket(a, ts, k, es) : -1;
+    ek[k] = bk[k] >= 0 ? ts.le[k] : -1;
     rb[k] = 0;
     re[k] = 0;
-    if (in) {
-      int le = -1;
-      bk[k] = pair_bucket(a, t, k, a2, &wk[k], &le);
-      ek[k] = bk[k] >= 0 ? le : -1;
-    }
+  }
+  // the block's bucket and expert bases of every slot in one round of loads (slot 0's key
+  // where a slot is not local: in range, unused)
+  int bb[kTopK], cb[kTopK];
+#pragma unroll
+  for (int k = 0; k < kTopK; k++) {
+    bb[k] = a.bcnt[(size_t)blockIdx.x * E3 + max(bk[k], 0)];
+    cb[k] = a.ccnt[(size_t)blockIdx.x * E + max(ek[k], 0)];
   }
   wave_key_ranks(bk, rb, bmask[wave]);
   wave_key_ranks(ek, re, emask[wave]);
@@ -262,14 +299,14 @@ __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a)
   for (int k = 0; k < kTopK; k++) {
     if (bk[k] < 0) continue;
     n_local++;
-    int pos = a.bcnt[(size_t)blockIdx.x * E3 + bk[k]] + rb[k];
-    int cpos = a.ccnt[(size_t)blockIdx.x * E + ek[k]] + re[k];
+    int pos = bb[k] + rb[k];
+    int cpos = cb[k] + re[k];
     for (int w = 0; w < wave; w++) {
       pos += (int)__popcll(bmask[w][bk[k]]);
       cpos += (int)__popcll(emask[w][ek[k]]);
     }
     a.perm_token[pos] = t;
-    a.perm_w[pos] = wk[k];
+    a.perm_w[pos] = ts.w[k];
     a.canon_token[cpos] = t;
     // slot = rank of the local expert among the token's local experts: the combine adds a
     // token's rows in ascending expert order
