@@ -8,10 +8,12 @@
 
 namespace moefp8 {
 
-// Workgroup = (token, 1024 columns), 4 columns per thread.
-constexpr int kCombineCols = 1024;
+// Workgroup = (token, 512 columns), 4 columns per thread (measured at T = 8192: 65 µs, against 67
+// with 1024 columns, 72 with 256, and 81 with 4 tokens x 1024 columns of 16 per lane).
+constexpr int kCombineCols = 512;
+constexpr int kCombineThreads = kCombineCols / 4;
 
-__global__ __launch_bounds__(256) void combine_kernel(const int* __restrict__ tok_slot,
+__global__ __launch_bounds__(kCombineThreads) void combine_kernel(const int* __restrict__ tok_slot,
                                                       const int* __restrict__ info,
                                                       const float* __restrict__ obuf,
                                                       void* __restrict__ out, int H, const void* shared,
@@ -64,7 +66,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const int* __restrict__ to
 
 void launch_combine(const Plan& pl, const float* obuf, void* out, int T, int H, hipStream_t stream) {
   if (T <= 0) return;
-  hipLaunchKernelGGL(combine_kernel, dim3(T, (H + kCombineCols - 1) / kCombineCols), dim3(256), 0, stream,
+  hipLaunchKernelGGL(combine_kernel, dim3(T, (H + kCombineCols - 1) / kCombineCols), dim3(kCombineThreads), 0, stream,
                      pl.tok_slot, pl.info, obuf, out, H, pl.shared, pl.shared_dt, pl.out_f32);
 }
 
