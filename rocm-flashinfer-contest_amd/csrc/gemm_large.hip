@@ -1081,13 +1081,16 @@ __device__ __forceinline__ void widen16(const v4i& x, v8h& t0, v8h& t1) {
 // blocks whose rows reach past LDS row 64, 32, or not).  kTwo: C's lo term too.
 template <bool kTwo, int NT>
 __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
-                                               uint32_t ring_lds, const float* sw2_s, int e, const RowMap& rm,
-                                               int hc, float* __restrict__ obuf, int* queues, int* next_s,
-                                               int n_units) {
+                                               uint32_t ring_lds, const float* sw2_s, const float* pw_s, int e,
+                                               const RowMap& rm, int hc, float* __restrict__ obuf, int* queues,
+                                               int* next_s, int n_units) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
   constexpr int kOps = kTwo ? 7 : 5;   // DMAs per wavefront and stage: hi 2, lo 2, W2 2, row scales 1
   const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
-  const int wave = wave_index(), lane = lane_id(), lr = lane & 15, kg = lane >> 4;
+  // lane-dependent addresses are formed per unit (hoisted out of the unit loop, some of them spill)
+  int lane = lane_id();
+  asm volatile("" : "+v"(lane));
+  const int wave = wave_index(), lr = lane & 15, kg = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
   // DMA sources (per-lane byte offsets): hi and lo rows 16w + 8q + (lane / 8), 8 slots per row;
   // W2 rows 32w + 16q + (lane / 4), 4 slots per row; row scales 64 (w % 2) + lane
@@ -1200,7 +1203,7 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
       const int R = 16 * t + 4 * kg + r;
       if (rm.valid(R)) {
         const int p = rm.src(R);
-        const float w = pl.perm_w[p];
+        const float w = pw_s[R];
 #pragma unroll
         for (int n = 0; n < 4; n++) obuf[(size_t)p * H + hc * kB2Cols + 64 * wn + 16 * n + lr] = acc[i][n][r] * w;
       }
@@ -1213,6 +1216,7 @@ __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2
     Problem pb, Plan pl, CHalf8 ch, float* __restrict__ obuf) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kB2Stages * kB2Stage];
   __shared__ float sw2_s[2 * kBigMaxKB];
+  __shared__ float pw_s[kBgRows];
   const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock, HC = H / kB2Cols;
   __shared__ int next_s;
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
@@ -1228,17 +1232,19 @@ __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2
     const bool two = uniform(pl.two_term[mb]) != 0;
     // the previous unit's readers are done with the ring and sw2_s, and every thread has read next_s
     __syncthreads();
-    // W2 block scales of the unit's two 128-column blocks, per 128-K block
+    const RowMap rm = row_map(row0, rows, flags);
+    // W2 block scales of the unit's two 128-column blocks, per 128-K block, and the routing weight
+    // of each LDS row's pair (for the epilogue), in one round of loads
     {
       const int t = threadIdx.x;
       if (t < 2 * KB) sw2_s[t] = pb.s2[((size_t)e * HB + 2 * hc + (t & 1)) * KB + (t >> 1)];
+      if (t < kBgRows) pw_s[t] = pl.perm_w[rm.src(t)];
     }
     __syncthreads();
-    const RowMap rm = row_map(row0, rows, flags);
     // LDS rows in use: [0, rows), and a mixed block's exact rows up to row 127
     const int top = (flags & kFlagMixed) ? kBgRows : rows;
 #define MOEFP8_G2_UNIT(TWO, NT) \
-  gemm2_big_unit<TWO, NT>(pb, pl, ch, ring, ring_lds, sw2_s, e, rm, hc, obuf, queues, &next_s, n_units)
+  gemm2_big_unit<TWO, NT>(pb, pl, ch, ring, ring_lds, sw2_s, pw_s, e, rm, hc, obuf, queues, &next_s, n_units)
     if (two) {
       if (top <= 32) MOEFP8_G2_UNIT(true, 1);
       else if (top <= 64) MOEFP8_G2_UNIT(true, 2);
