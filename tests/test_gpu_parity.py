@@ -293,6 +293,37 @@ def test_golden_fixtures_full_path():
         assert_close(out, ref, f.name)
 
 
+@pytest.mark.parametrize("T,E_local,H,I,shared", [(300, 16, 512, 256, False), (1100, 32, 256, 128, False),
+                                                    (300, 16, 512, 256, True)])
+def test_rows_without_local_pair_overwrite_stale_output(T, E_local, H, I, shared):
+    """Rows of tokens without a local pair on the 128-row path: exact zeros (or bf16 of the shared
+    row) written by the combine.  The output buffer is filled with NaN before each of two calls, so
+    a row nobody writes cannot pass as a zero left there by the allocator."""
+    from moe_fp8 import _abi
+    from moe_fp8.main import Runner
+    print(f"[stale output] T={T} E_local={E_local} H={H} I={I} shared={shared}", flush=True)
+    assert _abi.load().moefp8_path(T, E_local, H, I) == _abi.PATH_ROWS128
+    wl = W.Workload(f"z{T}", T, 4000 + T)
+    weights = W.make_weights(E_local, H, I, device="cpu", seed=5 + E_local)
+    args = boosted(W.make_inputs(wl, device="cpu", E_local=E_local, H=H, I=I, weights=weights), E_local, 0)
+    ref32, _ = O.moe_forward(*args)
+    sh = torch.randn(T, H, generator=torch.Generator().manual_seed(T)) if shared else None
+    if shared:
+        ref32 = ref32 + sh
+    ridx, _, _, _ = oracle_route(args[0], args[1])
+    nolocal = torch.from_numpy(~np.any((ridx >= 0) & (ridx < E_local), axis=1))
+    assert 0 < int(nolocal.sum()) < T
+    runner = Runner(*to_dev(args), shared_output=sh.to(DEV) if shared else None)
+    for call in range(2):
+        runner.out.fill_(float("nan"))
+        out = runner()
+        torch.cuda.synchronize()
+        assert_close(out, ref32, f"call {call}")
+        rows = out.cpu()[nolocal].float()
+        want = sh[nolocal].to(torch.bfloat16).float() if shared else torch.zeros_like(rows)
+        assert torch.equal(rows, want)
+
+
 def test_deterministic_and_inputs_untouched():
     T, E_local, H, I = 700, 32, 256, 128
     wl = W.Workload("det", T, 5)
