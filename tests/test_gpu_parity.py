@@ -293,16 +293,19 @@ def test_golden_fixtures_full_path():
         assert_close(out, ref, f.name)
 
 
-@pytest.mark.parametrize("T,E_local,H,I,shared", [(300, 16, 512, 256, False), (1100, 32, 256, 128, False),
-                                                    (300, 16, 512, 256, True)])
-def test_rows_without_local_pair_overwrite_stale_output(T, E_local, H, I, shared):
-    """Rows of tokens without a local pair on the 128-row path: exact zeros (or bf16 of the shared
-    row) written by the combine.  The output buffer is filled with NaN before each of two calls, so
-    a row nobody writes cannot pass as a zero left there by the allocator."""
+@pytest.mark.parametrize("T,E_local,H,I,shared,path", [(300, 16, 512, 256, False, 2), (1100, 32, 256, 128, False, 2),
+                                                         (300, 16, 512, 256, True, 2), (16, 32, 512, 256, False, 0),
+                                                         (40, 16, 256, 128, True, 0), (100, 32, 512, 256, False, 1),
+                                                         (100, 32, 512, 256, True, 1)])
+def test_rows_without_local_pair_overwrite_stale_output(T, E_local, H, I, shared, path):
+    """Rows of tokens without a local pair: exact zeros (or bf16 of the shared row), written by the
+    small-T GEMM2's epilogue (path 0) or by the combine (paths 1 and 2).  The output buffer is
+    filled with NaN before each of two calls, so a row nobody writes cannot pass as a zero left
+    there by the allocator."""
     from moe_fp8 import _abi
     from moe_fp8.main import Runner
     print(f"[stale output] T={T} E_local={E_local} H={H} I={I} shared={shared}", flush=True)
-    assert _abi.load().moefp8_path(T, E_local, H, I) == _abi.PATH_ROWS128
+    assert _abi.load().moefp8_path(T, E_local, H, I) == path
     wl = W.Workload(f"z{T}", T, 4000 + T)
     weights = W.make_weights(E_local, H, I, device="cpu", seed=5 + E_local)
     args = boosted(W.make_inputs(wl, device="cpu", E_local=E_local, H=H, I=I, weights=weights), E_local, 0)
