@@ -22,7 +22,8 @@ Prints ONE JSON line.  Headline: T=16 decode (H=7168, I=2048, 32 local experts),
 in us/call; the T=8192 large-prefill line and the other synthetic workloads
 are reported inside the same object.  ``cpu_baseline`` times the CPU oracle
 (fp32 torch, all local experts dequantised up front like the contest reference)
-on the host cores for one call of the headline workload.
+on the host cores: one warmup call and five timed calls of the headline workload,
+median with min / max, on the affine cores (capped at OMP_NUM_THREADS when set).
 """
 from __future__ import annotations
 
@@ -250,7 +251,9 @@ def copy_calibration():
     return 0
 
 
-def cpu_baseline(wl, weights_cpu, threads):
+def cpu_baseline(wl, weights_cpu, threads, affinity, reps=5):
+    """The CPU oracle on the host cores: one warmup call, then `reps` timed calls of the headline
+    workload; value = median, with min / max.  `threads` = torch's intra-op threads used."""
     import torch
     sys.path.insert(0, str(ROOT / "oracle"))
     import moe_oracle
@@ -258,12 +261,18 @@ def cpu_baseline(wl, weights_cpu, threads):
 
     torch.set_num_threads(threads)
     act = W.make_activations(wl, device="cpu")
-    t0 = time.perf_counter()
     moe_oracle.moe_forward(*act, *weights_cpu, 0, W.RSF, dequant_all_upfront=True)
-    dt = time.perf_counter() - t0
-    return dict(value=dt * 1e6, unit="us/call", cores=threads, kind="port",
-                sample=f"1 call of {wl.name} (T={wl.T}, H=7168, I=2048, 32 local experts): fp32 torch-CPU oracle, "
-                       f"all 32 experts dequantised up front as in the contest reference; {threads} threads")
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        moe_oracle.moe_forward(*act, *weights_cpu, 0, W.RSF, dequant_all_upfront=True)
+        times.append((time.perf_counter() - t0) * 1e6)
+    return dict(value=statistics.median(times), unit="us/call", cores=threads, kind="port",
+                median=statistics.median(times), min=min(times), max=max(times), reps=reps, warmup=1,
+                affinity_cores=affinity,
+                sample=f"{reps} calls of {wl.name} (T={wl.T}, H=7168, I=2048, 32 local experts) after 1 warmup call: "
+                       f"fp32 torch-CPU oracle, all 32 experts dequantised up front as in the contest reference "
+                       f"(~11 GB of fp32 weights); {threads} intra-op threads of {affinity} affine cores")
 
 
 def measure_quantize(T, steps, flush, H=7168):
@@ -336,10 +345,15 @@ def main():
               f"({quant['t8192']['hbm_frac']:.2f} of HBM)", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
-        threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+        # the process's CPU share: the affine cores, capped at OMP_NUM_THREADS where the environment
+        # sets it (16 per GPU on the measurement boxes, whatever the affinity mask shows)
+        affinity = len(os.sched_getaffinity(0))
+        cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+        threads = max(1, min(affinity, cap) if cap > 0 else affinity)
         weights_cpu = tuple(x.cpu() for x in weights)
-        cpu = cpu_baseline(wls[args.workload], weights_cpu, threads)
-        print(f"# cpu baseline: {cpu['value']:.0f} us/call on {threads} threads", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(wls[args.workload], weights_cpu, threads, affinity)
+        print(f"# cpu baseline: median {cpu['median']:.0f} us/call (min {cpu['min']:.0f}, max {cpu['max']:.0f}, "
+              f"{cpu['reps']} reps) on {threads} threads of {affinity} affine cores", file=sys.stderr, flush=True)
 
     line = {
         "metric": f"moe_fp8 block-scale MoE latency, {args.workload} (T={head['T']}, H=7168, I=2048, 32 local experts)",

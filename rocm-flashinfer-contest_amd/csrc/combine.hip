@@ -17,7 +17,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const int* __r
                                                       const int* __restrict__ info,
                                                       const float* __restrict__ obuf,
                                                       void* __restrict__ out, int H, const void* shared,
-                                                      int shared_dt, int out_f32) {
+                                                      int shared_dt, int out_f32, int pair_rows) {
   const int t = blockIdx.x;
   const int c = blockIdx.y * kCombineCols + 4 * threadIdx.x;
   const int S = info[4];
@@ -30,7 +30,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const int* __r
     float4 v[kTopK];
 #pragma unroll
     for (int k = 0; k < kTopK; k++)
-      v[k] = slots[k] >= 0 ? *reinterpret_cast<const float4*>(obuf + (size_t)slots[k] * H + c)
+      v[k] = slots[k] >= 0 ? *reinterpret_cast<const float4*>(obuf + (size_t)clamp_index(slots[k], pair_rows) * H + c)
                            : float4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < kTopK; k++) {
@@ -44,7 +44,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const int* __r
     // K-split partials of each pair row, added split by split, then pair by pair
     for (int k = 0; k < kTopK; k++) {
       if (slots[k] < 0) break;
-      const float* row = obuf + (size_t)slots[k] * S * H + c;
+      const float* row = obuf + (size_t)clamp_index(slots[k], pair_rows) * S * H + c;
       float4 o = *reinterpret_cast<const float4*>(row);
       for (int s = 1; s < S; s++) {
         const float4 v = *reinterpret_cast<const float4*>(row + (size_t)s * H);
@@ -67,7 +67,7 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const int* __r
 void launch_combine(const Plan& pl, const float* obuf, void* out, int T, int H, hipStream_t stream) {
   if (T <= 0) return;
   hipLaunchKernelGGL(combine_kernel, dim3(T, (H + kCombineCols - 1) / kCombineCols), dim3(kCombineThreads), 0, stream,
-                     pl.tok_slot, pl.info, obuf, out, H, pl.shared, pl.shared_dt, pl.out_f32);
+                     pl.tok_slot, pl.info, obuf, out, H, pl.shared, pl.shared_dt, pl.out_f32, pl.pair_rows);
 }
 
 }  // namespace moefp8

@@ -35,14 +35,16 @@ struct DecodePlanScratch {
   float esig[2 * kEGlobal];             // weight-scale estimates of each local expert
 };
 
-// K-split of a decode GEMM: the largest S in {8, 4, 2} whose units still fit the grid and
-// the partial rows, at least ceil(kb / 64) (a unit holds the weight scales of its <= 64
-// K-blocks one per lane), else that minimum.
+// K-split of a decode GEMM: the largest S <= kb whose units still fit one resident round of the
+// grid (n_mt * ncb * S <= slots) and whose partial rows fit (S * P <= rows_cap), and at least
+// ceil(kb / 64) (a unit holds the weight scales of its <= 64 K-blocks one per lane).  With one or
+// two pairs (T = 1 or 4) this spreads one expert's weights over every workgroup slot.
 __device__ __forceinline__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap) {
   const int s_min = (kb + kWave - 1) / kWave;
-  for (int S = 8; S > s_min; S >>= 1)
-    if ((int64_t)n_mt * ncb * S <= slots && (int64_t)S * P <= rows_cap && S <= kb) return S;
-  return s_min;
+  int S = kb;
+  if (n_mt > 0 && ncb > 0) S = min(S, slots / (n_mt * ncb));
+  if (P > 0) S = min(S, rows_cap / P);
+  return max(S, s_min);
 }
 
 // Builds the plan in `L` using `X` (every thread of a workgroup of kPlanThreads takes part;

@@ -207,7 +207,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
     const uint8_t* bp = pb.w13 + ((size_t)e * I2 + cg * 16 + lr) * H + (size_t)kb0 * kBlock + kg * 32;
     const float* swp = pb.s13 + ((size_t)e * (I2 / kBlock) + (cg * 16) / kBlock) * KB + kb0;
     // rows >= M repeat the m-tile's first pair (real data, results discarded)
-    const int tok = plan.tok[row0 + (lr < M ? lr : 0)];
+    const int tok = clamp_index(plan.tok[row0 + (lr < M ? lr : 0)], T);
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 
     if (!(flags & kFlagExactProducts) && M <= kPreRows && n <= kPreMaxKB) {
@@ -243,11 +243,11 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
         for (int q = 0; q < kPer; q++) {
           const int i = min((int)threadIdx.x + q * 64 * kDecBlockWaves, nch - 1);
           const int r = i / (n * 8), c = i - r * n * 8;
-          v[q] = *reinterpret_cast<const v4i*>(pb.hidden + (size_t)plan.tok[row0 + r] * H + (size_t)kb0 * kBlock +
-                                               c * 16);
+          v[q] = *reinterpret_cast<const v4i*>(pb.hidden + (size_t)clamp_index(plan.tok[row0 + r], T) * H +
+                                               (size_t)kb0 * kBlock + c * 16);
         }
         const int si = min((int)threadIdx.x, M * n - 1), sr = si / n, sj = si - sr * n;
-        const float sv = pb.hscale[(size_t)(kb0 + sj) * T + plan.tok[row0 + sr]];
+        const float sv = pb.hscale[(size_t)(kb0 + sj) * T + clamp_index(plan.tok[row0 + sr], T)];
 #pragma unroll
         for (int q = 0; q < kPer; q++) {
           const int i = threadIdx.x + q * 64 * kDecBlockWaves;
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
       // draining all of them).  Activation loads in the MFMA layout by every wavefront (16
       // rows x 64 bytes per instruction) cost the weight stream ~20% (measured).
       const int ar = 8 * (wave & 1) + (lane >> 3);
-      const int atok = plan.tok[row0 + (ar < M ? ar : 0)];
+      const int atok = clamp_index(plan.tok[row0 + (ar < M ? ar : 0)], T);
       const uint8_t* asrc =
           wave < 2 ? pb.hidden + (size_t)atok * H + (size_t)kb0 * kBlock + (lane & 7) * 16 : pb.hidden;
       const int astep = wave < 2 ? kBlock : 0;
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int dr = 4 * kg + r;
-        tok_d[r] = plan.tok[row0 + (dr < M ? dr : 0)];
+        tok_d[r] = clamp_index(plan.tok[row0 + (dr < M ? dr : 0)], T);
       }
       const uint8_t* ap = pb.hidden + (size_t)tok * H + (size_t)kb0 * kBlock + kg * 32;
       for (int j = 0; j < n; j++) {
@@ -401,10 +401,11 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
 // Combine of output columns [c0, c0 + 64) for every token by one workgroup (main.py:241-243):
 // each token's pair rows in ascending local-expert order (tok_slot), the K-split partials of
 // a row first, summed from zero in fp32 and rounded once to bf16; tokens without a local
-// expert get zeros.  Thread = (token, 4 columns).
+// expert get zeros.  Thread = (token, 4 columns).  Pair indices read from tok_slot are clamped below
+// pair_rows (the call's pair count: rows pair_rows * S of the partials are written).
 __device__ void combine_columns(const int* __restrict__ tok_slot, const float* __restrict__ obuf,
                                 void* __restrict__ out, int T, int H, int S, int c0, const void* shared,
-                                int shared_dt, int out_f32) {
+                                int shared_dt, int out_f32, int pair_rows) {
   constexpr int kQuads = 16;                            // 4-column groups of the 64 columns
   const int c = c0 + 4 * (threadIdx.x % kQuads);
   for (int t = threadIdx.x / kQuads; t < T; t += blockDim.x / kQuads) {
@@ -417,7 +418,7 @@ __device__ void combine_columns(const int* __restrict__ tok_slot, const float* _
       float2 lo[kTopK], hi[kTopK];
 #pragma unroll
       for (int k = 0; k < kTopK; k++) {
-        const float* r = obuf + (size_t)max(slots[k], 0) * H + c;
+        const float* r = obuf + (size_t)clamp_index(max(slots[k], 0), pair_rows) * H + c;
         lo[k] = load_shared_f32x2(r);
         hi[k] = load_shared_f32x2(r + 2);
       }
@@ -433,7 +434,7 @@ __device__ void combine_columns(const int* __restrict__ tok_slot, const float* _
     }
     for (int k = 0; S > 1 && k < kTopK; k++) {
       if (slots[k] < 0) break;
-      const float* row = obuf + (size_t)slots[k] * S * H + c;
+      const float* row = obuf + (size_t)clamp_index(slots[k], pair_rows) * S * H + c;
       float4 o = {0.f, 0.f, 0.f, 0.f};                 // the row's splits, in order
       for (int s0 = 0; s0 < S; s0 += kTopK) {
         float2 lo[kTopK], hi[kTopK];                    // up to 8 splits loaded together
@@ -681,7 +682,8 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     // output columns [64 cb, 64 cb + 64) are complete once all n_mt * S units of the column
     // block stored their rows
     if (arrive_last(pl.counters2 + du.cb, n_mt * S, &last_s))
-      combine_columns(pl.tok_slot, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves, pl.shared, pl.shared_dt, pl.out_f32);
+      combine_columns(pl.tok_slot, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves, pl.shared, pl.shared_dt,
+                      pl.out_f32, pl.info[0]);
   }
 }
 

@@ -234,11 +234,11 @@ __device__ __forceinline__ void gemm1_large_pass(const Problem& pb, const Plan& 
 #pragma unroll
   for (int r = 0; r < L::kDmaA; r++) {
     const int row = 16 * ((wave >> 1) + 2 * r) + lr;
-    const int tok = pl.perm_token[row0 + min(row, rows - 1)];
+    const int tok = clamp_index(pl.perm_token[row0 + min(row, rows - 1)], T);
     asrc[r] = pb.hidden + (size_t)tok * H + (4 * (wave & 1) + kg) * 16;
   }
   const int srow = min(64 * wave + lane, rows - 1);
-  const float* ssrc = pb.hscale + pl.perm_token[row0 + srow];
+  const float* ssrc = pb.hscale + clamp_index(pl.perm_token[row0 + srow], T);
 #pragma unroll
   for (int i = 0; i < NA; i++)
 #pragma unroll
@@ -501,7 +501,7 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
 #pragma unroll
   for (int q = 0; q < 2; q++) {
     const int r = 16 * wave + 8 * q + drow;
-    const int tok = pl.perm_token[row0 + min(r, rows - 1)];
+    const int tok = clamp_index(pl.perm_token[row0 + min(r, rows - 1)], T);
     aoff[q] = (uint32_t)tok * (uint32_t)H + (uint32_t)((dslot ^ slot_key8(r)) * 16);
   }
 #pragma unroll
@@ -511,7 +511,8 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
     const int wrow = (n < 2 ? 0 : I) + cb * kBlock + 32 * g + 16 * (n & 1) + rr;
     boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ slot_key8(R)) * 16);
   }
-  const uint32_t soff = 4u * (uint32_t)pl.perm_token[row0 + min(64 * (wave & 1) + lane, rows - 1)];
+  const uint32_t soff =
+      4u * (uint32_t)clamp_index(pl.perm_token[row0 + min(64 * (wave & 1) + lane, rows - 1)], T);
   const uint8_t* wbase = pb.w13 + (size_t)e * 2 * I * H;
   auto issue = [&](int j) {
     const int k = min(j, KB - 1);
@@ -653,7 +654,7 @@ __device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Pl
 #pragma unroll
   for (int q = 0; q < 2; q++) {
     const int r = 16 * wave + 8 * q + drow;
-    const int tok = pl.perm_token[rm.src(r)];
+    const int tok = clamp_index(pl.perm_token[rm.src(r)], T);
     aoff[q] = (uint32_t)tok * (uint32_t)H + (uint32_t)((dslot ^ slot_key8(r)) * 16);
   }
 #pragma unroll
@@ -663,7 +664,7 @@ __device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Pl
     const int wrow = (n < 2 ? 0 : I) + cb * kBlock + 32 * g + 16 * (n & 1) + rr;
     boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ slot_key8(R)) * 16);
   }
-  const uint32_t soff = 4u * (uint32_t)pl.perm_token[rm.src(64 * (wave & 1) + lane)];
+  const uint32_t soff = 4u * (uint32_t)clamp_index(pl.perm_token[rm.src(64 * (wave & 1) + lane)], T);
   const uint8_t* wbase = pb.w13 + (size_t)e * 2 * I * H;
   auto issue = [&](int j) {
     const int k = min(j, KB - 1);
@@ -1098,14 +1099,15 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
 #pragma unroll
   for (int q = 0; q < 2; q++) {
     const int r = 16 * wave + 8 * q + (lane >> 3);
-    hoff[q] = (uint32_t)rm.src(r) * (uint32_t)(2 * I) + (uint32_t)((((lane & 7) ^ slot_key8(r))) * 16);
+    hoff[q] = (uint32_t)clamp_index(rm.src(r), pl.pair_rows) * (uint32_t)(2 * I) +
+              (uint32_t)((((lane & 7) ^ slot_key8(r))) * 16);
   }
 #pragma unroll
   for (int q = 0; q < 2; q++) {
     const int R = 32 * wave + 16 * q + (lane >> 2);
     woff[q] = (uint32_t)(hc * kB2Cols + R) * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(R))) * 16);
   }
-  const uint32_t soff = 4u * (uint32_t)(rm.src(64 * (wave & 1) + lane) * KB);
+  const uint32_t soff = 4u * (uint32_t)(clamp_index(rm.src(64 * (wave & 1) + lane), pl.pair_rows) * KB);
   const uint8_t* wbase = pb.w2 + (size_t)e * H * I;
   auto issue = [&](int j) {
     const int k = min(j, KS - 1);

@@ -162,9 +162,10 @@ int num_compute_units() {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// fp32 logits are read as float4 rows; 16-bit inputs element by element.
+// The routing kernel reads logits and bias 4 elements at a time with 8-byte loads (load4_as_f32):
+// fp32 tensors must be 16-byte aligned, 16-bit ones 8-byte aligned.
 static bool aligned_for_dtype(const void* p, int dt) {
-  return ((uintptr_t)p & (dt == 0 ? 15u : 1u)) == 0;
+  return ((uintptr_t)p & (dt == 0 ? 15u : 7u)) == 0;
 }
 
 static int check_sizes(int64_t T, int E_local, int H, int I) {
@@ -330,6 +331,7 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
   pl.shared = a->shared_output;
   pl.shared_dt = a->shared_dtype;
   pl.out_f32 = a->output_f32;
+  pl.pair_rows = (int)L.pmax;
   float* tok_a2 = reinterpret_cast<float*>(ws + L.tok_a2);
   float* esig = reinterpret_cast<float*>(ws + L.esig);
 

@@ -114,6 +114,11 @@ __device__ __forceinline__ bool needs_exact_products(float a2, float w, float s1
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
+// An index read from the permutation tables (a token, or a pair row), clamped to [0, n) where it
+// becomes a load or DMA address (one VALU op; negative values clamp to n - 1): a wrong table
+// entry then shows as a parity failure instead of a memory fault.
+__device__ __forceinline__ int clamp_index(int i, int n) { return (int)min((uint32_t)i, (uint32_t)(n - 1)); }
+
 // LDS slot swizzles of 16-byte chunks: chunk c of row r sits in slot c ^ key(r).  The keys are
 // linear in the row bits and were chosen so that the MFMA operand reads (lanes = 16 rows x chunk
 // groups) and the row-order writes of the stages below are conflict-free whether the LDS serves

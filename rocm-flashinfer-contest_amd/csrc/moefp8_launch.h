@@ -76,6 +76,8 @@ struct Plan {
   const void* shared;         // optional [T, H] rows added before the bf16 rounding (NULL: none)
   int shared_dt;              // 0 fp32, 1 bf16
   int out_f32;                // output in fp32 (the sum before its bf16 rounding) instead of bf16
+  int pair_rows;              // pair rows the workspace holds (perm_token, C, O): pair indices read
+                              // from the tables are clamped below it where they become addresses
 };
 
 struct Problem {

@@ -20,6 +20,7 @@ over experts in ascending order; bf16 output.
 """
 from __future__ import annotations
 
+import collections
 import ctypes
 
 import torch
@@ -47,11 +48,15 @@ _DT = {torch.float32: _abi.DTYPE_F32, torch.bfloat16: _abi.DTYPE_BF16, torch.flo
 
 # Workspace bytes per (T, E_local, H, I), and reusable workspaces per (device, stream) for calls
 # whose workspace is at most _WS_KEEP_MAX bytes (the small-T decode sizes of a serving loop): calls
-# on one stream run in stream order, so they can share one buffer.  Larger workspaces come from the
-# torch allocator on every call (it caches them itself) and are not held between calls.
+# on one stream run in stream order, so they can share one buffer.  At most _WS_KEEP_PER_DEVICE
+# of them are held per device, the least recently used one dropped first (a server that makes a
+# stream per request does not grow device memory, and a reused stream handle only finds a buffer
+# that its stream order already protects).  Larger workspaces come from the torch allocator on
+# every call (it caches them itself) and are not held between calls.
 _WS_BYTES = {}
-_WS_KEEP = {}
+_WS_KEEP = collections.OrderedDict()
 _WS_KEEP_MAX = 64 << 20
+_WS_KEEP_PER_DEVICE = 4
 
 
 def _workspace(lib, device, stream, T, E_local, Hd, Id):
@@ -62,9 +67,13 @@ def _workspace(lib, device, stream, T, E_local, Hd, Id):
     if nbytes > _WS_KEEP_MAX:
         return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device), nbytes
     skey = (device.index, stream)
-    ws = _WS_KEEP.get(skey)
+    ws = _WS_KEEP.pop(skey, None)
     if ws is None or ws.numel() < nbytes:
-        ws = _WS_KEEP[skey] = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+    _WS_KEEP[skey] = ws                       # most recently used last
+    same_dev = [k for k in _WS_KEEP if k[0] == device.index]
+    for k in same_dev[:max(0, len(same_dev) - _WS_KEEP_PER_DEVICE)]:
+        del _WS_KEEP[k]
     return ws, nbytes
 
 
@@ -79,7 +88,12 @@ def _routing_input(x, name, device):
         raise ValueError(f"{name} is on {x.device}, expected {device}")
     if x.dtype not in _DT:
         raise TypeError(f"{name}: unsupported dtype {x.dtype} (float32, bfloat16 or float16)")
-    return x.contiguous()
+    x = x.contiguous()
+    # the routing kernel loads 4 elements at a time (8-byte loads): fp32 rows must start on 16
+    # bytes, 16-bit ones on 8; a view at another storage offset is copied
+    if x.data_ptr() % (16 if x.dtype == torch.float32 else 8) != 0:
+        x = x.clone()
+    return x
 
 
 def _fp8_input(x, name, device):

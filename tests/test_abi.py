@@ -101,6 +101,11 @@ def test_run_rejects_bad_arguments_before_any_launch(lib):
     assert run(_args(gemm2_weights_scale=None)) == -1
     assert run(_args(hidden_states=0x100001)) == -4
     assert run(_args(routing_logits=0x100002)) == -4              # fp32 logits need 16-byte rows
+    assert run(_args(routing_logits=0x100008)) == -4
+    # 16-bit routing inputs are read with 8-byte loads: 8-byte alignment
+    assert run(_args(routing_bias=0x200002, bias_dtype=1)) == -4            # 2-byte offset bf16 bias
+    assert run(_args(routing_bias=0x200004, bias_dtype=2)) == -4            # 4-byte offset f16 bias
+    assert run(_args(routing_logits=0x100002, logits_dtype=1)) == -4        # bf16 logits
     assert run(_args(gemm1_weights_scale=0x100002)) == -4
     assert run(_args(shared_output=0x100000 * 12, shared_dtype=2)) == -3   # shared rows: fp32 or bf16
     assert run(_args(shared_output=0x100008, shared_dtype=1)) == -4
@@ -116,6 +121,8 @@ def test_route_rejects_bad_arguments(lib):
     assert f(0x1000, 9, 0x2000, 1, 4, 2.5, 0x3000, 0x4000, None) == -3
     assert f(None, 0, 0x2000, 1, 4, 2.5, 0x3000, 0x4000, None) == -1
     assert f(0x1000, 0, 0x2000, 1, 0, 2.5, 0x3000, 0x4000, None) == 0
+    assert f(0x1000, 0, 0x2002, 1, 4, 2.5, 0x3000, 0x4000, None) == -4   # bf16 bias: 8-byte aligned
+    assert f(0x1008, 0, 0x2000, 1, 4, 2.5, 0x3000, 0x4000, None) == -4   # fp32 logits: 16-byte aligned
 
 
 def test_python_entry_point_fails_loudly_without_device_tensors(lib):

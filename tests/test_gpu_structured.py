@@ -71,7 +71,7 @@ def build(kind, T, seed, w_cpu):
 
 
 @pytest.mark.parametrize("kind", ["aligned", "aligned_block", "outliers", "both", "amplified"])
-@pytest.mark.parametrize("T", [48, 400])
+@pytest.mark.parametrize("T", [48, 100, 400])   # the small-T, grouped 16*MT-row and 128-row paths
 def test_structured_activations(weights, kind, T):
     print(f"[structured] {kind} T={T}", flush=True)
     w_dev, w_cpu = weights
