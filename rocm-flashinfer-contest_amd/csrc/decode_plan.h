@@ -35,13 +35,16 @@ struct DecodePlanScratch {
   float esig[2 * kEGlobal];             // weight-scale estimates of each local expert
 };
 
-// K-split of a decode GEMM: the largest S <= kb whose units still fit one resident round of the
-// grid (n_mt * ncb * S <= slots) and whose partial rows fit (S * P <= rows_cap), and at least
-// ceil(kb / 64) (a unit holds the weight scales of its <= 64 K-blocks one per lane).  With one or
-// two pairs (T = 1 or 4) this spreads one expert's weights over every workgroup slot.
+// K-split of a decode GEMM: the largest S <= kDecMaxSplit whose units still fit one resident round
+// of the grid (n_mt * ncb * S <= slots) and whose partial rows fit (S * P <= rows_cap), and at
+// least ceil(kb / 64) (a unit holds the weight scales of its <= 64 K-blocks one per lane).  More
+// splits fill more of the grid at T = 1 or 4 but lengthen the reduction each group's last unit
+// does (measured at T = 1 / T = 4 with one and two pairs: S <= 4 31.6 / 38.9 us per call, S <= 8
+// 34.3 / 44.4, up to 20 splits 35.4 / 41.4 even with the counters on separate lines).
+constexpr int kDecMaxSplit = 4;
 __device__ __forceinline__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap) {
   const int s_min = (kb + kWave - 1) / kWave;
-  int S = kb;
+  int S = min(kb, kDecMaxSplit);
   if (n_mt > 0 && ncb > 0) S = min(S, slots / (n_mt * ncb));
   if (P > 0) S = min(S, rows_cap / P);
   return max(S, s_min);

@@ -382,7 +382,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
     // blocks 2j, 2j + 1 ("up") and NCB/2 + 2j, NCB/2 + 2j + 1 ("gate"), S K-splits each.
     // Every unit publishes its partials and counts itself in; the last one forms C.
     const int j = (du.cb % (NCB / 2)) / 2;
-    if (arrive_last(pl.counters + du.g * (I / kBlock) + j, 4 * S, &last_s)) {
+    if (arrive_last(pl.counters + (du.g * (I / kBlock) + j) * kCounterStride, 4 * S, &last_s)) {
       const float sigma2 = da.esig[2 * e + 1];
       for (int r = wave; r < M; r += kDecBlockWaves) {
         // the pair's routing weight: its token's slot holding this expert (the routing outputs
@@ -392,7 +392,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
 #pragma unroll
         for (int k = 0; k < kTopK; k++)
           if (da.topk_ids[t * kTopK + k] - da.offset == e) w = da.topk_w[t * kTopK + k];
-        swiglu_block(I, S, row0 + r, j, gbuf, ch, w, sigma2, pl.two_term + du.g);
+        swiglu_block(I, S, row0 + r, j, gbuf, ch, w, sigma2, pl.two_term + du.g * kCounterStride);
       }
     }
   }
@@ -501,7 +501,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     const int lr = lane & 15, kg = lane >> 4;
     const DecUnit du = decode_unit(u, S, NCB);
     // the m-tile and GEMM1's measured flag loaded together (not the flag behind the tile's test)
-    const int measured = pl.two_term[du.g];
+    const int measured = pl.two_term[du.g * kCounterStride];
     const int4 mt = pl.mtiles[du.g];
     const int e = uniform(mt.x), row0 = uniform(mt.y), M = uniform(mt.z);
     // both f16 terms of C: predicted (the plan), or measured by GEMM1
@@ -681,7 +681,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     }
     // output columns [64 cb, 64 cb + 64) are complete once all n_mt * S units of the column
     // block stored their rows
-    if (arrive_last(pl.counters2 + du.cb, n_mt * S, &last_s))
+    if (arrive_last(pl.counters2 + du.cb * kCounterStride, n_mt * S, &last_s))
       combine_columns(pl.tok_slot, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves, pl.shared, pl.shared_dt,
                       pl.out_f32, pl.info[0]);
   }

@@ -84,10 +84,11 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
     L.rows_cap = pmax * smin > r8 ? pmax * smin : r8;
     L.mtiles = take((size_t)L.max_mtiles * 16);
     // arrival counters: per (m-tile, 128 C columns) for GEMM1, then per output column block,
-    // then GEMM2's precision flag per m-tile (all zeroed by the routing kernel)
+    // then GEMM2's precision flag per m-tile (all zeroed by the routing kernel), one 128-byte
+    // line each
     L.n_counters1 = L.max_mtiles * (I / kBlock);
     L.n_counters = L.n_counters1 + H / (16 * decode_unit_groups());
-    L.counters = take((size_t)(L.n_counters + L.max_mtiles) * 4);
+    L.counters = take((size_t)(L.n_counters + L.max_mtiles) * 4 * kCounterStride);
     L.gbuf = take((size_t)L.rows_cap * 2 * I * 4);
     L.c16 = take((size_t)L.c_plane * 2 * 2);
     L.c16_scale = take((size_t)pmax * (I / kBlock) * 4);
@@ -360,8 +361,8 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
                             decode_grid2(), H / (16 * groups),     I / kBlock, (int)L.rows_cap};
     pl.mtiles = reinterpret_cast<const int4*>(ws + L.mtiles);
     pl.counters = reinterpret_cast<int*>(ws + L.counters);
-    pl.counters2 = pl.counters + L.n_counters1;
-    pl.two_term = pl.counters + L.n_counters;
+    pl.counters2 = pl.counters + L.n_counters1 * kCounterStride;
+    pl.two_term = pl.counters + L.n_counters * kCounterStride;
     DecodePlanArgs da;
     da.topk_ids = topk_ids;
     da.topk_w = topk_w;

@@ -25,8 +25,8 @@ struct SplitPolicy {
 };
 
 // Routing of every token (main.py:139-165): topk_ids [T,8] ascending, topk_w [T,8];
-// with `mag`, also the magnitude estimates; zeroes zero[0, n_zero) (arrival counters of
-// the small-T GEMMs) on the way.
+// with `mag`, also the magnitude estimates; zeroes zero[i * kCounterStride] for i < n_zero
+// (arrival counters and flags of the small-T GEMMs) on the way.
 void launch_route(const void* logits, int logits_dt, const void* bias, int bias_dt, int64_t T, float rsf,
                   int* topk_ids, float* topk_w, const MagInputs* mag, int* zero, int n_zero, hipStream_t stream);
 
@@ -69,6 +69,7 @@ struct Plan {
   const int* canon_token;     // token of each pair in canonical (expert, token) order
   int* counters;              // small T: arrivals per (m-tile, 128 C columns), zeroed by the routing
   int* counters2;             // small T: arrivals per 64 output columns, zeroed by the routing
+                              // (small-T counters and flags: kCounterStride ints apart)
   const float* esig;          // [E, 2] W13 and W2 entry scale estimates of each local expert (routing)
   int* two_term;              // GEMM2's precision flags from measured C (needs_two_terms): per m-tile
                               // at small T (zeroed by the routing, set by GEMM1), per m-block at large T
@@ -107,6 +108,10 @@ void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, flo
 
 constexpr int kUnitQueues = 16;
 constexpr int kQueueStride = 64;   // ints between queue counters: one 256-byte line each
+// Small-T arrival counters and GEMM2 precision flags sit kCounterStride ints apart (one 128-byte
+// line each): device-scope atomics from many workgroups on one line serialise (measured at T = 1:
+// GEMM1 29 -> 18 us with 80 arrivals on each of 16 counters of one line).
+constexpr int kCounterStride = 32;
 
 // Large-T path (T > 64).  Permutation arguments: pair counts per (block of 256 tokens,
 // bucket = local expert x magnitude class) and the outputs of the three launches.

@@ -269,7 +269,8 @@ __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __rest
     return;
   }
   const int tb = (int)blockIdx.x - sigma_blocks - norm_blocks;   // routing block
-  for (int i = tb * kSigmaThreads + threadIdx.x; i < n_zero; i += token_blocks * kSigmaThreads) zero[i] = 0;
+  for (int i = tb * kSigmaThreads + threadIdx.x; i < n_zero; i += token_blocks * kSigmaThreads)
+    zero[(size_t)i * kCounterStride] = 0;
   // the first token's logits (a clamped row: no branch) leave with the bias, one round trip
   // for both; each later token's logits are loaded while the current one is routed
   const int64_t t0 = (int64_t)tb * kWavesPerBlock + wave, stride = (int64_t)token_blocks * kWavesPerBlock;
