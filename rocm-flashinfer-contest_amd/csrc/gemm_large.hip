@@ -1078,12 +1078,21 @@ __device__ __forceinline__ void widen16(const v4i& x, v8h& t0, v8h& t1) {
   }
 }
 
+// GEMM2's rows of a unit: LDS row R holds pair rowp[R] (staged in LDS from the row table, rows
+// past the block's last repeating it: computed, never stored).
+struct G2Rows {
+  const int* rowp;
+  int rows;
+  __device__ __forceinline__ int src(int R) const { return rowp[R]; }
+  __device__ __forceinline__ bool valid(int R) const { return R < rows; }
+};
+
 // One unit.  Wavefront (wm, wn) computes m-tiles NT wm .. NT wm + NT - 1 (NT = 4, 2 or 1 for
 // blocks whose rows reach past LDS row 64, 32, or not).  kTwo: C's lo term too.
 template <bool kTwo, int NT>
 __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float* sw2_s, const float* pw_s, int e,
-                                               const RowMap& rm, int hc, float* __restrict__ obuf, int* queues,
+                                               const G2Rows& rm, int hc, float* __restrict__ obuf, int* queues,
                                                int* next_s, int n_units) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
   constexpr int kOps = kTwo ? 7 : 5;   // DMAs per wavefront and stage: hi 2, lo 2, W2 2, row scales 1
@@ -1213,47 +1222,52 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
   }
 }
 
-// Units (m-block, 256 output columns) over GEMM2's blocks.
+// Units (m-block, 256 output columns) over GEMM2's own row table (Plan::g2_*): an expert's
+// one-term blocks, then its two-term blocks.
 __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm2_big_kernel(
     Problem pb, Plan pl, CHalf8 ch, float* __restrict__ obuf) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kB2Stages * kB2Stage];
   __shared__ float sw2_s[2 * kBigMaxKB];
   __shared__ float pw_s[kBgRows];
+  __shared__ int rowp_s[kBgRows];
   const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock, HC = H / kB2Cols;
   __shared__ int next_s;
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
-  const int n_units = pl.info[2] * HC;
+  const int n_units = pl.g2_ctl[2 * pb.E_local + 1] * HC;
   int* queues = pl.queues + 8 * kQueueStride;
   if (threadIdx.x == 0) next_s = first_unit(queues, n_units);
   __syncthreads();
   for (int v = uniform(next_s); v >= 0; v = uniform(next_s)) {
-    const int2 uc = unit_at(pl.mbgroup, v, HC);
+    const int2 uc = unit_at(pl.g2_group, v, HC);
     const int mb = uniform(uc.x), hc = uniform(uc.y);
-    const int4 blk = pl.mblocks[mb];
-    const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
-    const bool two = uniform(pl.two_term[mb]) != 0;
-    // the previous unit's readers are done with the ring and sw2_s, and every thread has read next_s
+    const int4 blk = pl.g2_blocks[mb];
+    const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z);
+    const bool two = uniform(blk.w) != 0;
+    // the previous unit's readers are done with the ring, sw2_s, pw_s and rowp_s, and every thread
+    // has read next_s
     __syncthreads();
-    const RowMap rm = row_map(row0, rows, flags);
-    // W2 block scales of the unit's two 128-column blocks, per 128-K block, and the routing weight
-    // of each LDS row's pair (for the epilogue), in one round of loads
+    // W2 block scales of the unit's two 128-column blocks, per 128-K block, and each LDS row's pair
+    // and routing weight (for the DMA sources and the epilogue)
     {
       const int t = threadIdx.x;
       if (t < 2 * KB) sw2_s[t] = pb.s2[((size_t)e * HB + 2 * hc + (t & 1)) * KB + (t >> 1)];
-      if (t < kBgRows) pw_s[t] = pl.perm_w[rm.src(t)];
+      if (t < kBgRows) {
+        const int p = clamp_index(pl.g2_pair[row0 + min(t, rows - 1)], pl.pair_rows);
+        rowp_s[t] = p;
+        pw_s[t] = pl.perm_w[p];
+      }
     }
     __syncthreads();
-    // LDS rows in use: [0, rows), and a mixed block's exact rows up to row 127
-    const int top = (flags & kFlagMixed) ? kBgRows : rows;
+    const G2Rows rm{rowp_s, rows};
 #define MOEFP8_G2_UNIT(TWO, NT) \
   gemm2_big_unit<TWO, NT>(pb, pl, ch, ring, ring_lds, sw2_s, pw_s, e, rm, hc, obuf, queues, &next_s, n_units)
     if (two) {
-      if (top <= 32) MOEFP8_G2_UNIT(true, 1);
-      else if (top <= 64) MOEFP8_G2_UNIT(true, 2);
+      if (rows <= 32) MOEFP8_G2_UNIT(true, 1);
+      else if (rows <= 64) MOEFP8_G2_UNIT(true, 2);
       else MOEFP8_G2_UNIT(true, 4);
     } else {
-      if (top <= 32) MOEFP8_G2_UNIT(false, 1);
-      else if (top <= 64) MOEFP8_G2_UNIT(false, 2);
+      if (rows <= 32) MOEFP8_G2_UNIT(false, 1);
+      else if (rows <= 64) MOEFP8_G2_UNIT(false, 2);
       else MOEFP8_G2_UNIT(false, 4);
     }
 #undef MOEFP8_G2_UNIT
@@ -1302,6 +1316,109 @@ __global__ __launch_bounds__(256) void c_flags_kernel(Plan pl, CHalf8 ch, int I)
 void launch_c_flags(const Plan& pl, const CHalf8& ch, int I, int max_blocks, hipStream_t stream) {
   if (max_blocks <= 0) return;
   hipLaunchKernelGGL(c_flags_kernel, dim3(max_blocks), dim3(256), 0, stream, pl, ch, I);
+}
+
+// GEMM2's row table for the 128-row path.  Thread = pair row p (GEMM1's row order): both f16
+// terms of C where its magnitude class is 1 or 2 (the estimate the permutation used, recomputed from
+// the same inputs) or where needs_two_terms holds on the largest of its C scales; its GEMM2 row is
+// claimed from the front (one term) or the back (two terms) of its expert's rows, through per-expert
+// counters, so that each expert's rows split into a one-term and a two-term group.  The order inside
+// a group depends on the claims, the results do not: every row is computed on its own.  The last
+// workgroup to arrive turns the counts into blocks of up to 128 rows.
+constexpr int kG2PlanThreads = 256;
+__global__ __launch_bounds__(kG2PlanThreads) void g2_plan_kernel(Plan pl, CHalf8 ch, const float* __restrict__ tok_a2,
+                                                                 int* __restrict__ g2_pair, int4* __restrict__ g2_blocks,
+                                                                 int2* __restrict__ g2_group, int T, int E, int I) {
+  __shared__ int cnt[2 * kEGlobal], base[2 * kEGlobal];
+  __shared__ int eoff[kEGlobal + 1];
+  __shared__ int last_s;
+  const int tid = threadIdx.x, P = pl.info[0];
+  const int p0 = blockIdx.x * kG2PlanThreads;
+  // workgroups past the last pair have nothing to place and do not arrive
+  if (p0 >= P) return;
+  const int n_arrive = (P + kG2PlanThreads - 1) / kG2PlanThreads;
+  const int p = p0 + tid, pc = min(p, P - 1), NCB = I / kBlock;
+  // the pair's inputs in one round of loads (clamped indices)
+  const int t = clamp_index(pl.perm_token[pc], T);
+  const float w = pl.perm_w[pc];
+  float smax = 0.f;
+  if (NCB % 4 == 0) {
+    for (int cb = 0; cb < NCB; cb += 4) {
+      const float4 s = *reinterpret_cast<const float4*>(ch.scale + (size_t)pc * NCB + cb);
+      smax = fmaxf(fmaxf(smax, fmaxf(s.x, s.y)), fmaxf(s.z, s.w));
+    }
+  } else {
+    for (int cb = 0; cb < NCB; cb++) smax = fmaxf(smax, ch.scale[(size_t)pc * NCB + cb]);
+  }
+  const float a2 = tok_a2[t];
+  for (int i = tid; i < 2 * E; i += kG2PlanThreads) cnt[i] = 0;
+  for (int i = tid; i <= E; i += kG2PlanThreads) eoff[i] = pl.expert_offsets[i];
+  __syncthreads();
+  // the pair's expert: the last e with eoff[e] <= pc (empty experts share their successor's offset)
+  int lo = 0, hi = E;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (eoff[mid] <= pc) lo = mid;
+    else hi = mid;
+  }
+  const int e = lo;
+  const float sqrt_i = sqrtf((float)I), s13 = pl.esig[2 * e], s2 = pl.esig[2 * e + 1];
+  const bool two = predicted_output_rms(a2, w, s13, s2, sqrt_i) > kOneTermRms ||
+                   needs_two_terms(w, s2, 448.0f * smax, sqrt_i);
+  const int key = 2 * e + (two ? 1 : 0);
+  int r = 0;
+  if (p < P) r = atomicAdd(&cnt[key], 1);
+  __syncthreads();
+  for (int i = tid; i < 2 * E; i += kG2PlanThreads)
+    if (cnt[i] > 0) base[i] = atomicAdd(&pl.g2_ctl[i], cnt[i]);
+  __syncthreads();
+  if (p < P) {
+    const int pos = two ? eoff[e + 1] - 1 - (base[key] + r) : eoff[e] + base[key] + r;
+    g2_pair[pos] = p;
+  }
+  // every thread's claims and row stores are issued; count this workgroup in
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    last_s = atomicAdd(&pl.g2_ctl[2 * E], 1) == n_arrive - 1;
+  }
+  __syncthreads();
+  if (!last_s) return;
+  __threadfence();
+  // the last workgroup: per-expert group sizes -> blocks {expert, first row, rows, two terms}
+  if (tid < kWave) {
+    const int lane = tid;
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += kWave) {
+      const int ee = e0 + lane;
+      int c1 = 0, c2 = 0;
+      if (ee < E) {
+        c1 = __hip_atomic_load(&pl.g2_ctl[2 * ee], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        c2 = __hip_atomic_load(&pl.g2_ctl[2 * ee + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      const int b1 = (c1 + kBgRows - 1) / kBgRows, b2 = (c2 + kBgRows - 1) / kBgRows, nb = b1 + b2;
+      const int first = carry + wave_exclusive_sum(nb);
+      for (int j = 0; j < b1; j++) {
+        g2_blocks[first + j] = int4{ee, eoff[ee] + kBgRows * j, min(kBgRows, c1 - kBgRows * j), 0};
+        g2_group[first + j] = int2{first, nb};
+      }
+      for (int j = 0; j < b2; j++) {
+        g2_blocks[first + b1 + j] = int4{ee, eoff[ee] + c1 + kBgRows * j, min(kBgRows, c2 - kBgRows * j), 1};
+        g2_group[first + b1 + j] = int2{first, nb};
+      }
+      carry = __builtin_amdgcn_readlane(first + nb, kWave - 1);
+    }
+    if (lane == 0) pl.g2_ctl[2 * E + 1] = carry;
+  }
+}
+
+void launch_g2_plan(const Problem& pb, const Plan& pl, const CHalf8& ch, const float* tok_a2, int pmax,
+                    hipStream_t stream) {
+  if (pmax <= 0) return;
+  const int grid = (pmax + kG2PlanThreads - 1) / kG2PlanThreads;
+  hipLaunchKernelGGL(g2_plan_kernel, dim3(grid), dim3(kG2PlanThreads), 0, stream, pl, ch, tok_a2,
+                     const_cast<int*>(pl.g2_pair), const_cast<int4*>(pl.g2_blocks), const_cast<int2*>(pl.g2_group),
+                     pb.T, pb.E_local, pb.I);
 }
 
 // ------------------------------------------------------------------------------------------ launch

@@ -44,8 +44,9 @@ struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
   size_t tok_a2, esig, mtiles, counters, c16, c16_scale, gbuf, obuf;
   size_t canon_token, bcnt, ccnt, mblocks, mbgroup, two_term, queues, c_hi, c_lo16, c_scale;
+  size_t g2_pair, g2_blocks, g2_group, g2_ctl;
   size_t total;
-  int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks, n_counters1, n_counters;
+  int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks, max_blocks2, n_counters1, n_counters;
   int nblk;
 };
 
@@ -110,6 +111,12 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.mbgroup = take((size_t)L.max_blocks * 8);
   L.two_term = take((size_t)L.max_blocks * 4);
   L.queues = take((size_t)kUnitQueues * kQueueStride * 4);
+  // GEMM2's row table (128-row path): its blocks split each expert's rows in two groups
+  L.max_blocks2 = (pmax + kBigRows - 1) / kBigRows + 2 * (int64_t)E_local;
+  L.g2_pair = take((size_t)pmax * 4);
+  L.g2_blocks = take((size_t)L.max_blocks2 * 16);
+  L.g2_group = take((size_t)L.max_blocks2 * 8);
+  L.g2_ctl = take((size_t)(2 * E_local + 2) * 4);
   L.c_hi = take((size_t)pmax * I * 2);
   L.c_lo16 = take((size_t)pmax * I * 2);
   L.c_scale = take((size_t)pmax * (I / kBlock) * 4);
@@ -329,6 +336,10 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
   pl.counters2 = nullptr;
   pl.esig = reinterpret_cast<const float*>(ws + L.esig);
   pl.two_term = nullptr;
+  pl.g2_pair = nullptr;
+  pl.g2_blocks = nullptr;
+  pl.g2_group = nullptr;
+  pl.g2_ctl = nullptr;
   pl.shared = a->shared_output;
   pl.shared_dt = a->shared_dtype;
   pl.out_f32 = a->output_f32;
@@ -433,6 +444,11 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
   pl.mbgroup = pa.mbgroup;
   pl.queues = pa.queues;
   pl.two_term = reinterpret_cast<int*>(ws + L.two_term);
+  pl.g2_pair = reinterpret_cast<const int*>(ws + L.g2_pair);
+  pl.g2_blocks = reinterpret_cast<const int4*>(ws + L.g2_blocks);
+  pl.g2_group = reinterpret_cast<const int2*>(ws + L.g2_group);
+  pl.g2_ctl = reinterpret_cast<int*>(ws + L.g2_ctl);
+  pa.g2_ctl = big ? pl.g2_ctl : nullptr;
   CHalf8 ch;
   ch.hi = reinterpret_cast<_Float16*>(ws + L.c_hi);
   ch.lo16 = reinterpret_cast<_Float16*>(ws + L.c_lo16);
@@ -450,11 +466,16 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
     launch_gemm1_large(pb, pl, ch, large_mt(T), (int)(L.max_blocks * (I / kBlock)), s);
   }
   mark(3);
-  // GEMM2's precision per m-block from the C that GEMM1 wrote (the activation stage)
-  launch_c_flags(pl, ch, I, (int)L.max_blocks, s);
+  // GEMM2's precision from the C that GEMM1 wrote (the activation stage): per pair, with GEMM2's
+  // own row table, on the 128-row path; per m-block otherwise
+  if (big) {
+    launch_g2_plan(pb, pl, ch, tok_a2, (int)L.pmax, s);
+  } else {
+    launch_c_flags(pl, ch, I, (int)L.max_blocks, s);
+  }
   mark(4);
   if (big) {
-    launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks * (H / 256)), s);
+    launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks2 * (H / 256)), s);
   } else {
     launch_gemm2_large(pb, pl, ch, obuf, large_mt(T), (int)(L.max_blocks * (H / kBlock)), s);
   }

@@ -187,6 +187,18 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return (readlane_f32(v, 0) + readlane_f32(v, 16)) + (readlane_f32(v, 32) + readlane_f32(v, 48));
 }
 
+// Exclusive prefix sum over the wavefront (Hillis-Steele on shuffles).
+__device__ __forceinline__ int wave_exclusive_sum(int v) {
+  const int lane = lane_id();
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off, kWave);
+    if (lane >= off) x += y;
+  }
+  return x - v;
+}
+
 // Number of set bits of m in lanes below this one.
 __device__ __forceinline__ int lanes_below(uint64_t m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));

@@ -79,6 +79,13 @@ struct Plan {
   int out_f32;                // output in fp32 (the sum before its bf16 rounding) instead of bf16
   int pair_rows;              // pair rows the workspace holds (perm_token, C, O): pair indices read
                               // from the tables are clamped below it where they become addresses
+  // 128-row path, GEMM2's own row table (built by the g2 plan launch from the C GEMM1 wrote): per
+  // expert its one-term rows, then its two-term rows, in blocks of up to 128
+  const int* g2_pair;         // [Pmax] GEMM2 row -> pair row
+  const int4* g2_blocks;      // {expert, first GEMM2 row, rows, two terms of C}
+  const int2* g2_group;       // per block {first block of its expert, the expert's blocks}
+  int* g2_ctl;                // [2 E_local] one- / two-term row counts per expert, then the plan's
+                              // arrival counter and the block count (zeroed by the permutation)
 };
 
 struct Problem {
@@ -136,6 +143,7 @@ struct LargePermArgs {
   int4* mblocks;        // m-blocks of both GEMMs {expert, first row, rows, flags}
   int2* mbgroup;        // per m-block: {first m-block of its expert, the expert's m-blocks}
   int* queues;          // [kUnitQueues * kQueueStride] unit queues of the grouped GEMMs, zeroed here
+  int* g2_ctl;          // [2 E_local + 2] GEMM2 row-table counters, zeroed here (NULL: none)
   int mixed;            // fold <= 32 exact-product rows into the expert's last class 0/1 block
   int rows_a;           // block height over an expert's class 0 and 1 rows
   int rows_b;           // block height over its class 2 (exact-product) rows
@@ -164,7 +172,12 @@ void launch_c_flags(const Plan& pl, const CHalf8& ch, int I, int max_blocks, hip
 // GEMM2 over the blocks [0, info[2]), taken 16 * mt rows at a time
 void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int mt, int max_units,
                         hipStream_t stream);
-// GEMM2 over the whole table, 256 output columns per unit
+// GEMM2's row table for the 128-row path (Plan::g2_*): every pair whose C needs both f16 terms
+// (its magnitude class, or needs_two_terms on the C scales GEMM1 wrote) goes to its expert's
+// two-term blocks, the others to its one-term blocks.  Pmax bounds the launch's pair rows.
+void launch_g2_plan(const Problem& pb, const Plan& pl, const CHalf8& ch, const float* tok_a2, int pmax,
+                    hipStream_t stream);
+// GEMM2 over its row table (Plan::g2_*), 256 output columns per unit
 void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int max_units,
                       hipStream_t stream);
 

@@ -117,18 +117,6 @@ __device__ __forceinline__ int upper_bound(const int* v, int n, int x) {
   return lo;
 }
 
-// Exclusive prefix sum over the wavefront (Hillis-Steele on shuffles).
-__device__ __forceinline__ int wave_exclusive_sum(int v) {
-  const int lane = lane_id();
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_up(x, off, kWave);
-    if (lane >= off) x += y;
-  }
-  return x - v;
-}
-
 constexpr int kScanLdsInts = 12288;   // 48 KB of staged counts
 
 __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a) {
@@ -137,6 +125,7 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
   __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], eb1[kEGlobal + 1];
   const int E = a.E_local, E3 = E * kClasses, nb = a.nblk, tid = threadIdx.x, lane = lane_id();
   if (tid < kUnitQueues) a.queues[tid * kQueueStride] = 0;
+  if (a.g2_ctl && tid < 2 * E + 2) a.g2_ctl[tid] = 0;
 
   // Per bucket: exclusive prefix of the raw counts over blocks (relative) and the total; per
   // expert: the same over its three buckets (the canonical per-block base).  The counts are
