@@ -1319,8 +1319,10 @@ void launch_c_flags(const Plan& pl, const CHalf8& ch, int I, int max_blocks, hip
 }
 
 // GEMM2's row table for the 128-row path.  Thread = pair row p (GEMM1's row order): both f16
-// terms of C where its magnitude class is 1 or 2 (the estimate the permutation used, recomputed from
-// the same inputs) or where needs_two_terms holds on the largest of its C scales; its GEMM2 row is
+// terms of C where needs_two_terms holds on the largest of its C scales (the measured bound q: a row
+// at or below kOneTermQ keeps its one-term error within the bound whatever its class), or where the
+// row took GEMM1's exact products (magnitude class 2, recomputed from the permutation's inputs: such
+// rows are large enough for either rounding to matter, and stay on 22 bits); its GEMM2 row is
 // claimed from the front (one term) or the back (two terms) of its expert's rows, through per-expert
 // counters, so that each expert's rows split into a one-term and a two-term group.  The order inside
 // a group depends on the claims, the results do not: every row is computed on its own.  The last
@@ -1363,7 +1365,7 @@ __global__ __launch_bounds__(kG2PlanThreads) void g2_plan_kernel(Plan pl, CHalf8
   }
   const int e = lo;
   const float sqrt_i = sqrtf((float)I), s13 = pl.esig[2 * e], s2 = pl.esig[2 * e + 1];
-  const bool two = predicted_output_rms(a2, w, s13, s2, sqrt_i) > kOneTermRms ||
+  const bool two = predicted_output_rms(a2, w, s13, s2, sqrt_i) > kPreciseRms ||
                    needs_two_terms(w, s2, 448.0f * smax, sqrt_i);
   const int key = 2 * e + (two ? 1 : 0);
   int r = 0;

@@ -71,7 +71,8 @@ __device__ __forceinline__ void split_f16(float x, float inv, _Float16& hi, _Flo
 // the measured rms ~7x).  Used before GEMM1, where only the inputs are known: pairs above
 // kPreciseRms take GEMM1's exact-product path (the fp8 MFMA's adder error is relative to
 // sum |a w|, which this estimate tracks), and pairs above kOneTermRms are grouped together inside
-// their expert and take two terms of C in GEMM2 (kFlagTwoTermC).
+// their expert and take two terms of C in GEMM2 (kFlagTwoTermC) on the small-T and grouped paths
+// (the 128-row path decides each row's terms from its measured C alone, g2_plan_kernel).
 constexpr float kPreciseRms = 96.0f;
 constexpr float kOneTermRms = 8.0f;
 constexpr uint8_t kFlagExactProducts = 1;
