@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define MOEFP8_ABI_VERSION 6
+#define MOEFP8_ABI_VERSION 7
 
 /* Operator constants (solutions/moe_fp8/main.py:22-29). */
 #define MOEFP8_E_GLOBAL 256
@@ -94,10 +94,12 @@ typedef struct moefp8_args {
   int32_t* permuted_tokens;
   /* optional, may be NULL: array of MOEFP8_NUM_STAGE_EVENTS hipEvent_t created by the
    * caller.  Event i is recorded on `stream` before stage i (route, permute, GEMM1,
-   * activation, GEMM2, combine; GEMM1 applies SwiGLU itself, so the activation stage is
-   * empty, and for T <= 64 GEMM2 also does the combine, leaving that stage empty too) and
-   * the last one after the combine, so stage i's device time is
-   * hipEventElapsedTime(ev[i], ev[i+1]).  Used for live per-kernel timing. */
+   * activation, GEMM2, combine, then GEMM2 and combine of the second half of the output
+   * columns; GEMM1 applies SwiGLU itself, so the activation stage is empty, for T <= 64 GEMM2
+   * also does the combine, leaving that stage empty too, and calls whose per-pair output rows
+   * fit the workspace in one pass leave the last two stages empty) and the last one after the
+   * last combine, so stage i's device time is hipEventElapsedTime(ev[i], ev[i+1]).  Used for
+   * live per-kernel timing. */
   void* stage_events;
   /* optional, may be NULL: [T, H] dense rows in shared_dtype (MOEFP8_DTYPE_F32 or
    * MOEFP8_DTYPE_BF16, 16-byte aligned) added to each token's routed sum in fp32 before its
@@ -114,7 +116,7 @@ typedef struct moefp8_args {
   int32_t output_f32;
 } moefp8_args;
 
-#define MOEFP8_NUM_STAGE_EVENTS 7
+#define MOEFP8_NUM_STAGE_EVENTS 9
 
 /* ABI version of the loaded library (MOEFP8_ABI_VERSION of its build). */
 int moefp8_abi_version(void);
@@ -136,6 +138,15 @@ int moefp8_workspace_size(int64_t num_tokens, int32_t num_local_experts, int32_t
 #define MOEFP8_PATH_GROUPED 1
 #define MOEFP8_PATH_ROWS128 2
 int moefp8_path(int64_t num_tokens, int32_t num_local_experts, int32_t hidden_size, int32_t intermediate_size);
+
+/* Passes moefp8_run makes over the output columns for these sizes when the routing yields
+ * num_pairs local (token, expert) pairs (host only; no counterpart in the reference): 1, or 2 on
+ * the MOEFP8_PATH_ROWS128 path when the workspace's fp32 per-pair output rows cannot hold all
+ * columns of every pair.  Above 1 GiB for T x min(8, E_local) rows, the workspace holds rows for
+ * half that many pairs (T > 4681 at H = 7168, E_local >= 8); a call with more pairs runs GEMM2 and
+ * the combine once per half of the output columns.  A negative status for bad sizes. */
+int moefp8_output_passes(int64_t num_tokens, int32_t num_local_experts, int32_t hidden_size,
+                         int32_t intermediate_size, int64_t num_pairs);
 
 /* The operator: replaces solutions/moe_fp8/main.py:173-243 (run).
  * routing (main.py:139-165) -> token permutation (main.py:216-226) ->

@@ -12,26 +12,27 @@ namespace moefp8 {
 // with 1024 columns, 72 with 256, and 81 with 4 tokens x 1024 columns of 16 per lane).
 constexpr int kCombineCols = 512;
 constexpr int kCombineThreads = kCombineCols / 4;
+// Workgroups of the second output pass, which has nothing to do unless the call's pairs outnumber
+// its O rows.
+constexpr int kCombineSpareGrid = 256;
 
-__global__ __launch_bounds__(kCombineThreads) void combine_kernel(const int* __restrict__ tok_slot,
-                                                      const int* __restrict__ info,
-                                                      const float* __restrict__ obuf,
-                                                      void* __restrict__ out, int H, const void* shared,
-                                                      int shared_dt, int out_f32, int pair_rows) {
-  const int t = blockIdx.x;
-  const int c = blockIdx.y * kCombineCols + 4 * threadIdx.x;
-  const int S = info[4];
+// Token t's output columns [c, c + 4) (c inside [op.c0, op.c1)), from O rows [op.rows_cap][op.ocols]
+// holding the pass's columns from column 0.
+__device__ __forceinline__ void combine_quad(const int* __restrict__ tok_slot, const float* __restrict__ obuf,
+                                             void* __restrict__ out, int t, int c, int H, int S, const OutPass& op,
+                                             const void* shared, int shared_dt, int out_f32) {
+  const int oc = c - op.c0;
   int slots[kTopK];
 #pragma unroll
   for (int k = 0; k < kTopK; k++) slots[k] = tok_slot[(size_t)t * kTopK + k];
-  if (c >= H) return;
   float4 acc = {0.f, 0.f, 0.f, 0.f};
   if (S == 1) {
     float4 v[kTopK];
 #pragma unroll
     for (int k = 0; k < kTopK; k++)
-      v[k] = slots[k] >= 0 ? *reinterpret_cast<const float4*>(obuf + (size_t)clamp_index(slots[k], pair_rows) * H + c)
-                           : float4{0.f, 0.f, 0.f, 0.f};
+      v[k] = slots[k] >= 0
+                 ? *reinterpret_cast<const float4*>(obuf + (size_t)clamp_index(slots[k], op.rows_cap) * op.ocols + oc)
+                 : float4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < kTopK; k++) {
       if (slots[k] < 0) break;
@@ -44,10 +45,10 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const int* __r
     // K-split partials of each pair row, added split by split, then pair by pair
     for (int k = 0; k < kTopK; k++) {
       if (slots[k] < 0) break;
-      const float* row = obuf + (size_t)clamp_index(slots[k], pair_rows) * S * H + c;
+      const float* row = obuf + (size_t)clamp_index(slots[k], op.rows_cap) * S * op.ocols + oc;
       float4 o = *reinterpret_cast<const float4*>(row);
       for (int s = 1; s < S; s++) {
-        const float4 v = *reinterpret_cast<const float4*>(row + (size_t)s * H);
+        const float4 v = *reinterpret_cast<const float4*>(row + (size_t)s * op.ocols);
         o.x += v.x;
         o.y += v.y;
         o.z += v.z;
@@ -63,11 +64,57 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const int* __r
   store_out4(out, (size_t)t * H + c, acc, out_f32);
 }
 
+// Workgroup (token blockIdx.x, 512 columns blockIdx.y from the pass's first column): with pass < 0
+// all H columns from O rows [pair_rows][H], else the columns of output pass `pass` (out_pass).
+__global__ __launch_bounds__(kCombineThreads) void combine_kernel(const int* __restrict__ tok_slot,
+                                                      const int* __restrict__ info,
+                                                      const float* __restrict__ obuf,
+                                                      void* __restrict__ out, int H, int o_rows, int pass,
+                                                      const void* shared, int shared_dt, int out_f32,
+                                                      int pair_rows) {
+  OutPass op{0, H, H, pair_rows};
+  if (pass >= 0) op = out_pass(info[0], H, o_rows, pass, pair_rows);
+  const int c = op.c0 + blockIdx.y * kCombineCols + 4 * threadIdx.x;
+  if (c >= op.c1) return;
+  combine_quad(tok_slot, obuf, out, blockIdx.x, c, H, info[4], op, shared, shared_dt, out_f32);
+}
+
+// The same over a fixed grid (items (token, 512 columns), tokens fastest), for an output pass that
+// has columns only when the call's pairs outnumber O's rows: its workgroups exit at once otherwise.
+__global__ __launch_bounds__(kCombineThreads) void combine_spare_kernel(const int* __restrict__ tok_slot,
+                                                            const int* __restrict__ info,
+                                                            const float* __restrict__ obuf,
+                                                            void* __restrict__ out, int T, int H, int o_rows,
+                                                            int pass, const void* shared, int shared_dt,
+                                                            int out_f32, int pair_rows) {
+  const OutPass op = out_pass(info[0], H, o_rows, pass, pair_rows);
+  const int n_chunks = (op.c1 - op.c0 + kCombineCols - 1) / kCombineCols, S = info[4];
+  for (int64_t item = blockIdx.x; item < (int64_t)T * n_chunks; item += gridDim.x) {
+    const int t = (int)(item % T), chunk = (int)(item / T);
+    const int c = op.c0 + chunk * kCombineCols + 4 * threadIdx.x;
+    if (c < op.c1) combine_quad(tok_slot, obuf, out, t, c, H, S, op, shared, shared_dt, out_f32);
+  }
+}
 
 void launch_combine(const Plan& pl, const float* obuf, void* out, int T, int H, hipStream_t stream) {
   if (T <= 0) return;
   hipLaunchKernelGGL(combine_kernel, dim3(T, (H + kCombineCols - 1) / kCombineCols), dim3(kCombineThreads), 0, stream,
-                     pl.tok_slot, pl.info, obuf, out, H, pl.shared, pl.shared_dt, pl.out_f32, pl.pair_rows);
+                     pl.tok_slot, pl.info, obuf, out, H, 0, -1, pl.shared, pl.shared_dt, pl.out_f32, pl.pair_rows);
+}
+
+// Pass 0 (the single pass of nearly every call) takes one workgroup per (token, 512 columns) of
+// all H columns; pass 1 a fixed grid that exits at once unless the call's pairs outnumber O's rows.
+void launch_combine_pass(const Plan& pl, const float* obuf, void* out, int T, int H, int o_rows, int pass,
+                         hipStream_t stream) {
+  if (T <= 0) return;
+  if (pass == 0) {
+    hipLaunchKernelGGL(combine_kernel, dim3(T, (H + kCombineCols - 1) / kCombineCols), dim3(kCombineThreads), 0,
+                       stream, pl.tok_slot, pl.info, obuf, out, H, o_rows, 0, pl.shared, pl.shared_dt, pl.out_f32,
+                       pl.pair_rows);
+  } else {
+    hipLaunchKernelGGL(combine_spare_kernel, dim3(kCombineSpareGrid), dim3(kCombineThreads), 0, stream, pl.tok_slot,
+                       pl.info, obuf, out, T, H, o_rows, pass, pl.shared, pl.shared_dt, pl.out_f32, pl.pair_rows);
+  }
 }
 
 }  // namespace moefp8

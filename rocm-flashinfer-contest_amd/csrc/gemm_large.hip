@@ -1092,8 +1092,8 @@ struct G2Rows {
 template <bool kTwo, int NT>
 __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float* sw2_s, const float* pw_s, int e,
-                                               const G2Rows& rm, int hc, float* __restrict__ obuf, int* queues,
-                                               int* next_s, int n_units) {
+                                               const G2Rows& rm, int hc, float* __restrict__ obuf, int ocol0,
+                                               int ocols, int orows, int* queues, int* next_s, int n_units) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
   constexpr int kOps = kTwo ? 7 : 5;   // DMAs per wavefront and stage: hi 2, lo 2, W2 2, row scales 1
   const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
@@ -1213,36 +1213,75 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
     for (int r = 0; r < 4; r++) {
       const int R = 16 * t + 4 * kg + r;
       if (rm.valid(R)) {
-        const int p = rm.src(R);
+        const int p = clamp_index(rm.src(R), orows);
         const float w = pw_s[R];
 #pragma unroll
-        for (int n = 0; n < 4; n++) obuf[(size_t)p * H + hc * kB2Cols + 64 * wn + 16 * n + lr] = acc[i][n][r] * w;
+        for (int n = 0; n < 4; n++) obuf[(size_t)p * ocols + ocol0 + 64 * wn + 16 * n + lr] = acc[i][n][r] * w;
       }
     }
   }
 }
 
 // Units (m-block, 256 output columns) over GEMM2's own row table (Plan::g2_*): an expert's
-// one-term blocks, then its two-term blocks.
+// one-term blocks, then its two-term blocks; the column blocks of output pass `pass` (out_pass),
+// written to O rows of the pass's length from column 0; `pass` also picks the pass's unit queues.
 __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm2_big_kernel(
-    Problem pb, Plan pl, CHalf8 ch, float* __restrict__ obuf) {
+    Problem pb, Plan pl, CHalf8 ch, float* __restrict__ obuf, int o_rows, int pass) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[kB2Stages * kB2Stage];
   __shared__ float sw2_s[2 * kBigMaxKB];
   __shared__ float pw_s[kBgRows];
   __shared__ int rowp_s[kBgRows];
-  const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock, HC = H / kB2Cols;
+  // the row table's groups: per expert its first GEMM2 row, one- and two-term row counts, first block
+  __shared__ int g_off[kEGlobal + 1], g_c1[kEGlobal], g_c2[kEGlobal], g_first[kEGlobal + 1];
+  const int H = pb.H, I = pb.I, KB = I / kBlock, HB = H / kBlock, E = pb.E_local;
   __shared__ int next_s;
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
-  const int n_units = pl.g2_ctl[2 * pb.E_local + 1] * HC;
-  int* queues = pl.queues + 8 * kQueueStride;
+  const OutPass op = out_pass(pl.info[0], H, o_rows, pass, pl.pair_rows);
+  const int hc0 = op.c0 / kB2Cols, hcn = (op.c1 - op.c0) / kB2Cols, ocols = op.ocols;
+  // a pass without columns (the second, for a call whose pairs fit O's rows) ends here, before
+  // any queue is touched
+  if (hcn == 0) return;
+  for (int i = threadIdx.x; i <= E; i += blockDim.x) {
+    g_off[i] = pl.expert_offsets[i];
+    if (i < E) {
+      g_c1[i] = pl.g2_ctl[2 * i];
+      g_c2[i] = pl.g2_ctl[2 * i + 1];
+    }
+  }
+  __syncthreads();
+  // blocks of up to 128 rows per group, numbered expert by expert
+  if (threadIdx.x < kWave) {
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += kWave) {
+      const int ee = e0 + (int)threadIdx.x;
+      const int nb = ee < E ? (g_c1[ee] + kBgRows - 1) / kBgRows + (g_c2[ee] + kBgRows - 1) / kBgRows : 0;
+      const int first = carry + wave_exclusive_sum(nb);
+      if (ee < E) g_first[ee] = first;
+      carry = __builtin_amdgcn_readlane(first + nb, kWave - 1);
+    }
+    if (threadIdx.x == 0) g_first[E] = carry;
+  }
+  __syncthreads();
+  const int n_units = g_first[E] * hcn;
+  int* queues = pl.queues + (8 + 8 * pass) * kQueueStride;
   if (threadIdx.x == 0) next_s = first_unit(queues, n_units);
   __syncthreads();
   for (int v = uniform(next_s); v >= 0; v = uniform(next_s)) {
-    const int2 uc = unit_at(pl.g2_group, v, HC);
-    const int mb = uniform(uc.x), hc = uniform(uc.y);
-    const int4 blk = pl.g2_blocks[mb];
-    const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z);
-    const bool two = uniform(blk.w) != 0;
+    // unit v -> expert (the last whose first unit is <= v; empty experts share their successor's),
+    // then column block and block, the expert's blocks innermost; the block's group and rows
+    int lo = 0, hi = E;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (g_first[mid] * hcn <= v) lo = mid;
+      else hi = mid;
+    }
+    const int e = uniform(lo), nb = g_first[e + 1] - g_first[e], local = v - g_first[e] * hcn;
+    const int hcl = uniform(local / nb), hc = hc0 + hcl, b = local % nb;
+    const int c1 = g_c1[e], b1 = (c1 + kBgRows - 1) / kBgRows;
+    const bool two = uniform(b >= b1 ? 1 : 0) != 0;
+    const int j = two ? b - b1 : b;
+    const int row0 = uniform(g_off[e] + (two ? c1 : 0) + kBgRows * j);
+    const int rows = uniform(min(kBgRows, (two ? g_c2[e] : c1) - kBgRows * j));
     // the previous unit's readers are done with the ring, sw2_s, pw_s and rowp_s, and every thread
     // has read next_s
     __syncthreads();
@@ -1259,8 +1298,9 @@ __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2
     }
     __syncthreads();
     const G2Rows rm{rowp_s, rows};
-#define MOEFP8_G2_UNIT(TWO, NT) \
-  gemm2_big_unit<TWO, NT>(pb, pl, ch, ring, ring_lds, sw2_s, pw_s, e, rm, hc, obuf, queues, &next_s, n_units)
+#define MOEFP8_G2_UNIT(TWO, NT)                                                                               \
+  gemm2_big_unit<TWO, NT>(pb, pl, ch, ring, ring_lds, sw2_s, pw_s, e, rm, hc, obuf, hcl * kB2Cols, ocols,          \
+                          op.rows_cap, queues, &next_s, n_units)
     if (two) {
       if (rows <= 32) MOEFP8_G2_UNIT(true, 1);
       else if (rows <= 64) MOEFP8_G2_UNIT(true, 2);
@@ -1321,27 +1361,23 @@ void launch_c_flags(const Plan& pl, const CHalf8& ch, int I, int max_blocks, hip
 // GEMM2's row table for the 128-row path.  Thread = pair row p (GEMM1's row order): both f16
 // terms of C where needs_two_terms holds on the largest of its C scales (the measured bound q: a row
 // at or below kOneTermQ keeps its one-term error within the bound whatever its class), or where the
-// row took GEMM1's exact products (magnitude class 2, recomputed from the permutation's inputs: such
-// rows are large enough for either rounding to matter, and stay on 22 bits); its GEMM2 row is
-// claimed from the front (one term) or the back (two terms) of its expert's rows, through per-expert
-// counters, so that each expert's rows split into a one-term and a two-term group.  The order inside
-// a group depends on the claims, the results do not: every row is computed on its own.  The last
-// workgroup to arrive turns the counts into blocks of up to 128 rows.
+// row took GEMM1's exact products (magnitude class 2: the expert's rows from xrow[e] on; such rows
+// are large enough for either rounding to matter, and stay on 22 bits); its GEMM2 row is claimed
+// from the front (one term) or the back (two terms) of its expert's rows, through per-expert
+// counters, so that each expert's rows split into a one-term and a two-term group (GEMM2 cuts the
+// groups into blocks of up to 128 rows from the counts).  The order inside a group depends on the
+// claims, the results do not: every row is computed on its own.
 constexpr int kG2PlanThreads = 256;
-__global__ __launch_bounds__(kG2PlanThreads) void g2_plan_kernel(Plan pl, CHalf8 ch, const float* __restrict__ tok_a2,
-                                                                 int* __restrict__ g2_pair, int4* __restrict__ g2_blocks,
-                                                                 int2* __restrict__ g2_group, int T, int E, int I) {
+__global__ __launch_bounds__(kG2PlanThreads) void g2_plan_kernel(Plan pl, CHalf8 ch, int* __restrict__ g2_pair, int E,
+                                                                 int I) {
   __shared__ int cnt[2 * kEGlobal], base[2 * kEGlobal];
-  __shared__ int eoff[kEGlobal + 1];
-  __shared__ int last_s;
-  const int tid = threadIdx.x, P = pl.info[0];
-  const int p0 = blockIdx.x * kG2PlanThreads;
-  // workgroups past the last pair have nothing to place and do not arrive
-  if (p0 >= P) return;
-  const int n_arrive = (P + kG2PlanThreads - 1) / kG2PlanThreads;
-  const int p = p0 + tid, pc = min(p, P - 1), NCB = I / kBlock;
-  // the pair's inputs in one round of loads (clamped indices)
-  const int t = clamp_index(pl.perm_token[pc], T);
+  __shared__ int eoff[kEGlobal + 1], xs[kEGlobal];
+  __shared__ float sig2[kEGlobal];
+  const int tid = threadIdx.x, NCB = I / kBlock;
+  const int p = blockIdx.x * kG2PlanThreads + tid, pc = min(p, pl.pair_rows - 1);
+  // every input in one round of loads: the pair count, the pair's weight and C scales (rows past the
+  // call's pairs read in range and are ignored), the experts' offsets, first exact rows and W2 scales
+  const int P = pl.info[0];
   const float w = pl.perm_w[pc];
   float smax = 0.f;
   if (NCB % 4 == 0) {
@@ -1352,21 +1388,27 @@ __global__ __launch_bounds__(kG2PlanThreads) void g2_plan_kernel(Plan pl, CHalf8
   } else {
     for (int cb = 0; cb < NCB; cb++) smax = fmaxf(smax, ch.scale[(size_t)pc * NCB + cb]);
   }
-  const float a2 = tok_a2[t];
+  for (int i = tid; i <= E; i += kG2PlanThreads) {
+    eoff[i] = pl.expert_offsets[i];
+    if (i < E) {
+      xs[i] = pl.xrow[i];
+      sig2[i] = pl.esig[2 * i + 1];
+    }
+  }
   for (int i = tid; i < 2 * E; i += kG2PlanThreads) cnt[i] = 0;
-  for (int i = tid; i <= E; i += kG2PlanThreads) eoff[i] = pl.expert_offsets[i];
+  // workgroups past the last pair have nothing to place
+  if ((int)blockIdx.x * kG2PlanThreads >= P) return;
   __syncthreads();
-  // the pair's expert: the last e with eoff[e] <= pc (empty experts share their successor's offset)
+  // the pair's expert: the last e with eoff[e] <= p (empty experts share their successor's offset)
+  const int pp = min(p, P - 1);
   int lo = 0, hi = E;
   while (hi - lo > 1) {
     const int mid = (lo + hi) >> 1;
-    if (eoff[mid] <= pc) lo = mid;
+    if (eoff[mid] <= pp) lo = mid;
     else hi = mid;
   }
   const int e = lo;
-  const float sqrt_i = sqrtf((float)I), s13 = pl.esig[2 * e], s2 = pl.esig[2 * e + 1];
-  const bool two = predicted_output_rms(a2, w, s13, s2, sqrt_i) > kPreciseRms ||
-                   needs_two_terms(w, s2, 448.0f * smax, sqrt_i);
+  const bool two = pp >= xs[e] || needs_two_terms(w, sig2[e], 448.0f * smax, sqrtf((float)I));
   const int key = 2 * e + (two ? 1 : 0);
   int r = 0;
   if (p < P) r = atomicAdd(&cnt[key], 1);
@@ -1378,49 +1420,13 @@ __global__ __launch_bounds__(kG2PlanThreads) void g2_plan_kernel(Plan pl, CHalf8
     const int pos = two ? eoff[e + 1] - 1 - (base[key] + r) : eoff[e] + base[key] + r;
     g2_pair[pos] = p;
   }
-  // every thread's claims and row stores are issued; count this workgroup in
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    last_s = atomicAdd(&pl.g2_ctl[2 * E], 1) == n_arrive - 1;
-  }
-  __syncthreads();
-  if (!last_s) return;
-  __threadfence();
-  // the last workgroup: per-expert group sizes -> blocks {expert, first row, rows, two terms}
-  if (tid < kWave) {
-    const int lane = tid;
-    int carry = 0;
-    for (int e0 = 0; e0 < E; e0 += kWave) {
-      const int ee = e0 + lane;
-      int c1 = 0, c2 = 0;
-      if (ee < E) {
-        c1 = __hip_atomic_load(&pl.g2_ctl[2 * ee], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        c2 = __hip_atomic_load(&pl.g2_ctl[2 * ee + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      const int b1 = (c1 + kBgRows - 1) / kBgRows, b2 = (c2 + kBgRows - 1) / kBgRows, nb = b1 + b2;
-      const int first = carry + wave_exclusive_sum(nb);
-      for (int j = 0; j < b1; j++) {
-        g2_blocks[first + j] = int4{ee, eoff[ee] + kBgRows * j, min(kBgRows, c1 - kBgRows * j), 0};
-        g2_group[first + j] = int2{first, nb};
-      }
-      for (int j = 0; j < b2; j++) {
-        g2_blocks[first + b1 + j] = int4{ee, eoff[ee] + c1 + kBgRows * j, min(kBgRows, c2 - kBgRows * j), 1};
-        g2_group[first + b1 + j] = int2{first, nb};
-      }
-      carry = __builtin_amdgcn_readlane(first + nb, kWave - 1);
-    }
-    if (lane == 0) pl.g2_ctl[2 * E + 1] = carry;
-  }
 }
 
-void launch_g2_plan(const Problem& pb, const Plan& pl, const CHalf8& ch, const float* tok_a2, int pmax,
-                    hipStream_t stream) {
+void launch_g2_plan(const Problem& pb, const Plan& pl, const CHalf8& ch, int pmax, hipStream_t stream) {
   if (pmax <= 0) return;
   const int grid = (pmax + kG2PlanThreads - 1) / kG2PlanThreads;
-  hipLaunchKernelGGL(g2_plan_kernel, dim3(grid), dim3(kG2PlanThreads), 0, stream, pl, ch, tok_a2,
-                     const_cast<int*>(pl.g2_pair), const_cast<int4*>(pl.g2_blocks), const_cast<int2*>(pl.g2_group),
-                     pb.T, pb.E_local, pb.I);
+  hipLaunchKernelGGL(g2_plan_kernel, dim3(grid), dim3(kG2PlanThreads), 0, stream, pl, ch,
+                     const_cast<int*>(pl.g2_pair), pb.E_local, pb.I);
 }
 
 // ------------------------------------------------------------------------------------------ launch
@@ -1462,12 +1468,12 @@ void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, flo
   }
 }
 
-void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int max_units,
-                      hipStream_t stream) {
+void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int max_units, int o_rows,
+                      int pass, hipStream_t stream) {
   const int cus = num_compute_units();
   const int grid = max_units < cus ? max_units : cus;
   if (grid <= 0) return;
-  hipLaunchKernelGGL(gemm2_big_kernel, dim3(grid), dim3(kBgThreads), 0, stream, pb, pl, ch, obuf);
+  hipLaunchKernelGGL(gemm2_big_kernel, dim3(grid), dim3(kBgThreads), 0, stream, pb, pl, ch, obuf, o_rows, pass);
 }
 
 }  // namespace moefp8

@@ -37,6 +37,22 @@ bool large_big(int64_t T, int E_local, int H, int I) {
          T * H < ((int64_t)1 << 31) && pmax * 2 * I < ((int64_t)1 << 32);
 }
 int large_mt(int64_t T) { return T / 32 >= 48 ? 4 : 2; }
+
+// The 128-row path's fp32 per-pair output rows O: above this many bytes for Pmax rows (T > 4681 at
+// H = 7168 with E_local >= 8) the workspace holds ceil(Pmax / 2) rows of all H columns.  A call with
+// at most that many local pairs (every routing that averages up to 4 local experts per token; the
+// T = 8192 benchmark has 8,587 of 65,536) runs GEMM2 and the combine once over all columns; a call
+// with more runs them once per half of the columns (blocks of 256), each pass's rows then being
+// half as long.  W2 rows are output columns, so no weight is read twice.  The kernels take the
+// decision from the pair count on the device; the host launches both passes.
+constexpr size_t kOutRowsBudget = (size_t)1 << 30;
+int64_t output_rows(int64_t T, int E_local, int H, int I) {
+  const int64_t pmax = T * (E_local < kTopK ? E_local : kTopK);
+  if (T <= kDecodeMaxT || !large_big(T, E_local, H, I) || (size_t)pmax * H * 4 <= kOutRowsBudget) return pmax;
+  // rows of the first (larger) half of the columns for every pair: ceil(pmax * half / H) full rows
+  const int64_t half = (H / 256 + 1) / 2 * 256;
+  return (pmax * half + H - 1) / H;
+}
 int large_rows_a(int64_t T, int E, int H, int I) { return large_big(T, E, H, I) ? kBigRows : 16 * large_mt(T); }
 int large_rows_b(int64_t T, int E, int H, int I) { return large_big(T, E, H, I) ? kExactRows : 16 * large_mt(T); }
 
@@ -44,9 +60,10 @@ struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
   size_t tok_a2, esig, mtiles, counters, c16, c16_scale, gbuf, obuf;
   size_t canon_token, bcnt, ccnt, mblocks, mbgroup, two_term, queues, c_hi, c_lo16, c_scale;
-  size_t g2_pair, g2_blocks, g2_group, g2_ctl;
+  size_t g2_pair, g2_ctl, xrow;
   size_t total;
   int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks, max_blocks2, n_counters1, n_counters;
+  int64_t o_rows;
   int nblk;
 };
 
@@ -114,13 +131,13 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   // GEMM2's row table (128-row path): its blocks split each expert's rows in two groups
   L.max_blocks2 = (pmax + kBigRows - 1) / kBigRows + 2 * (int64_t)E_local;
   L.g2_pair = take((size_t)pmax * 4);
-  L.g2_blocks = take((size_t)L.max_blocks2 * 16);
-  L.g2_group = take((size_t)L.max_blocks2 * 8);
-  L.g2_ctl = take((size_t)(2 * E_local + 2) * 4);
+  L.g2_ctl = take((size_t)(2 * E_local) * 4);
+  L.xrow = take((size_t)E_local * 4);
   L.c_hi = take((size_t)pmax * I * 2);
   L.c_lo16 = take((size_t)pmax * I * 2);
   L.c_scale = take((size_t)pmax * (I / kBlock) * 4);
-  L.obuf = take((size_t)pmax * H * 4);
+  L.o_rows = output_rows(T, E_local, H, I);
+  L.obuf = take((size_t)L.o_rows * H * 4);
   L.total = o;
   return L;
 }
@@ -246,6 +263,14 @@ int moefp8_path(int64_t num_tokens, int32_t num_local_experts, int32_t hidden_si
                                                                                     : MOEFP8_PATH_GROUPED;
 }
 
+int moefp8_output_passes(int64_t num_tokens, int32_t num_local_experts, int32_t hidden_size,
+                         int32_t intermediate_size, int64_t num_pairs) {
+  const int rc = check_sizes(num_tokens, num_local_experts, hidden_size, intermediate_size);
+  if (rc) return rc;
+  if (num_pairs < 0) return MOEFP8_ERR_SHAPE;
+  return num_pairs > output_rows(num_tokens, num_local_experts, hidden_size, intermediate_size) ? 2 : 1;
+}
+
 int moefp8_route(const void* routing_logits, int32_t logits_dtype, const void* routing_bias, int32_t bias_dtype,
                  int64_t num_tokens, float routed_scaling_factor, int32_t* topk_ids, float* topk_weights,
                  void* stream) {
@@ -337,9 +362,8 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
   pl.esig = reinterpret_cast<const float*>(ws + L.esig);
   pl.two_term = nullptr;
   pl.g2_pair = nullptr;
-  pl.g2_blocks = nullptr;
-  pl.g2_group = nullptr;
   pl.g2_ctl = nullptr;
+  pl.xrow = nullptr;
   pl.shared = a->shared_output;
   pl.shared_dt = a->shared_dtype;
   pl.out_f32 = a->output_f32;
@@ -409,6 +433,8 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
     launch_gemm2_decode(pb, pl, ch, obuf, a->output, s);
     mark(5);
     mark(6);   // the combine is GEMM2's epilogue: empty combine stage
+    mark(7);   // one pass over the output columns: empty second-pass stages
+    mark(8);
     return finish(a, L, topk_ids, topk_w, pl, s);
   }
   // large T: routing, permutation (3 launches), GEMM1 (+SwiGLU, C split), GEMM2, combine
@@ -445,10 +471,10 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
   pl.queues = pa.queues;
   pl.two_term = reinterpret_cast<int*>(ws + L.two_term);
   pl.g2_pair = reinterpret_cast<const int*>(ws + L.g2_pair);
-  pl.g2_blocks = reinterpret_cast<const int4*>(ws + L.g2_blocks);
-  pl.g2_group = reinterpret_cast<const int2*>(ws + L.g2_group);
   pl.g2_ctl = reinterpret_cast<int*>(ws + L.g2_ctl);
   pa.g2_ctl = big ? pl.g2_ctl : nullptr;
+  pa.xrow = reinterpret_cast<int*>(ws + L.xrow);
+  pl.xrow = pa.xrow;
   CHalf8 ch;
   ch.hi = reinterpret_cast<_Float16*>(ws + L.c_hi);
   ch.lo16 = reinterpret_cast<_Float16*>(ws + L.c_lo16);
@@ -469,19 +495,28 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
   // GEMM2's precision from the C that GEMM1 wrote (the activation stage): per pair, with GEMM2's
   // own row table, on the 128-row path; per m-block otherwise
   if (big) {
-    launch_g2_plan(pb, pl, ch, tok_a2, (int)L.pmax, s);
+    launch_g2_plan(pb, pl, ch, (int)L.pmax, s);
   } else {
     launch_c_flags(pl, ch, I, (int)L.max_blocks, s);
   }
   mark(4);
   if (big) {
-    launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks2 * (H / 256)), s);
+    // GEMM2 and the combine over the output columns: one pass, or two when the call's pairs
+    // outnumber O's rows (the kernels decide from the pair count; a pass with nothing to do exits)
+    for (int pass = 0; pass < 2; pass++) {
+      launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks2 * (H / 256)), (int)L.o_rows, pass, s);
+      mark(5 + 2 * pass);
+      launch_combine_pass(pl, obuf, a->output, (int)T, H, (int)L.o_rows, pass, s);
+      mark(6 + 2 * pass);
+    }
   } else {
     launch_gemm2_large(pb, pl, ch, obuf, large_mt(T), (int)(L.max_blocks * (H / kBlock)), s);
+    mark(5);
+    launch_combine(pl, obuf, a->output, (int)T, H, s);
+    mark(6);
+    mark(7);
+    mark(8);
   }
-  mark(5);
-  launch_combine(pl, obuf, a->output, (int)T, H, s);
-  mark(6);
   return finish(a, L, topk_ids, topk_w, pl, s);
 }
 

@@ -80,12 +80,11 @@ struct Plan {
   int pair_rows;              // pair rows the workspace holds (perm_token, C, O): pair indices read
                               // from the tables are clamped below it where they become addresses
   // 128-row path, GEMM2's own row table (built by the g2 plan launch from the C GEMM1 wrote): per
-  // expert its one-term rows, then its two-term rows, in blocks of up to 128
+  // expert its one-term rows, then its two-term rows (GEMM2 takes them in blocks of up to 128)
   const int* g2_pair;         // [Pmax] GEMM2 row -> pair row
-  const int4* g2_blocks;      // {expert, first GEMM2 row, rows, two terms of C}
-  const int2* g2_group;       // per block {first block of its expert, the expert's blocks}
-  int* g2_ctl;                // [2 E_local] one- / two-term row counts per expert, then the plan's
-                              // arrival counter and the block count (zeroed by the permutation)
+  int* g2_ctl;                // [2 E_local] one- / two-term row counts per expert (zeroed by the
+                              // permutation)
+  const int* xrow;            // [E_local] first exact-product row of each local expert (permutation)
 };
 
 struct Problem {
@@ -113,7 +112,7 @@ void launch_gemm1_decode(const Problem& pb, const Plan& pl, const DecodePlanArgs
 void launch_gemm2_decode(const Problem& pb, const Plan& pl, const CHalf& ch, float* obuf, void* out,
                         hipStream_t stream);
 
-constexpr int kUnitQueues = 16;
+constexpr int kUnitQueues = 24;   // GEMM1 (0..7), GEMM2 by output-column pass (8..15, 16..23)
 constexpr int kQueueStride = 64;   // ints between queue counters: one 256-byte line each
 // Small-T arrival counters and GEMM2 precision flags sit kCounterStride ints apart (one 128-byte
 // line each): device-scope atomics from many workgroups on one line serialise (measured at T = 1:
@@ -143,7 +142,8 @@ struct LargePermArgs {
   int4* mblocks;        // m-blocks of both GEMMs {expert, first row, rows, flags}
   int2* mbgroup;        // per m-block: {first m-block of its expert, the expert's m-blocks}
   int* queues;          // [kUnitQueues * kQueueStride] unit queues of the grouped GEMMs, zeroed here
-  int* g2_ctl;          // [2 E_local + 2] GEMM2 row-table counters, zeroed here (NULL: none)
+  int* g2_ctl;          // [2 E_local] GEMM2 row-table counters, zeroed here (NULL: none)
+  int* xrow;            // [E_local] first exact-product (class 2) row of each local expert
   int mixed;            // fold <= 32 exact-product rows into the expert's last class 0/1 block
   int rows_a;           // block height over an expert's class 0 and 1 rows
   int rows_b;           // block height over its class 2 (exact-product) rows
@@ -175,13 +175,27 @@ void launch_gemm2_large(const Problem& pb, const Plan& pl, const CHalf8& ch, flo
 // GEMM2's row table for the 128-row path (Plan::g2_*): every pair whose C needs both f16 terms
 // (its magnitude class, or needs_two_terms on the C scales GEMM1 wrote) goes to its expert's
 // two-term blocks, the others to its one-term blocks.  Pmax bounds the launch's pair rows.
-void launch_g2_plan(const Problem& pb, const Plan& pl, const CHalf8& ch, const float* tok_a2, int pmax,
-                    hipStream_t stream);
-// GEMM2 over its row table (Plan::g2_*), 256 output columns per unit
-void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int max_units,
-                      hipStream_t stream);
+void launch_g2_plan(const Problem& pb, const Plan& pl, const CHalf8& ch, int pmax, hipStream_t stream);
+// Output-column pass `pass` (0 or 1) of a call whose O buffer holds o_rows rows of H floats: with at
+// most o_rows pairs, pass 0 covers all H columns (rows of H floats) and pass 1 nothing; with more,
+// each pass covers half of the column blocks of 256 (rows of H / 2 floats, rounded up to 256).
+struct OutPass {
+  int c0, c1, ocols, rows_cap;
+};
+__device__ __forceinline__ OutPass out_pass(int P, int H, int o_rows, int pass, int pair_rows) {
+  if (P <= o_rows) return pass == 0 ? OutPass{0, H, H, o_rows} : OutPass{H, H, H, o_rows};
+  const int half = (H / 256 + 1) / 2 * 256;
+  return pass == 0 ? OutPass{0, half, half, pair_rows} : OutPass{half, H, half, pair_rows};
+}
+// GEMM2 over its row table (Plan::g2_*), 256 output columns per unit, over the columns of output
+// pass `pass` (out_pass)
+void launch_gemm2_big(const Problem& pb, const Plan& pl, const CHalf8& ch, float* obuf, int max_units, int o_rows,
+                      int pass, hipStream_t stream);
 
 void launch_combine(const Plan& pl, const float* obuf, void* out, int T, int H, hipStream_t stream);
+// The combine of output pass `pass` (out_pass) of the 128-row path.
+void launch_combine_pass(const Plan& pl, const float* obuf, void* out, int T, int H, int o_rows, int pass,
+                         hipStream_t stream);
 
 // Per-token 1x128 e4m3 quantization of bf16 (x_dt 1) or fp32 (0) activations [T, H] into
 // q [T, H] and scale [H/128, T].

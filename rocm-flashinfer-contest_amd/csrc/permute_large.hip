@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
   __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], eb1[kEGlobal + 1];
   const int E = a.E_local, E3 = E * kClasses, nb = a.nblk, tid = threadIdx.x, lane = lane_id();
   if (tid < kUnitQueues) a.queues[tid * kQueueStride] = 0;
-  if (a.g2_ctl && tid < 2 * E + 2) a.g2_ctl[tid] = 0;
+  if (a.g2_ctl && tid < 2 * E) a.g2_ctl[tid] = 0;
 
   // Per bucket: exclusive prefix of the raw counts over blocks (relative) and the total; per
   // expert: the same over its three buckets (the canonical per-block base).  The counts are
@@ -185,6 +185,7 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
         eb1[e] = carry_1 + p1;
         a.expert_offsets[e] = carry + pn;
         a.mtile_offsets[e] = carry_mt + pmt;
+        a.xrow[e] = carry + pn + n0 + n1;
         if (n > 0) a.active[carry_act + lanes_below(act)] = e;
       }
       carry += __builtin_amdgcn_readlane(pn + n, kWave - 1);

@@ -12,7 +12,7 @@ from pathlib import Path
 LIB_NAME = "libmoefp8.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
@@ -31,8 +31,8 @@ STATUS = {
 }
 
 # Every extern "C" symbol of include/moefp8.h.
-EXPORTS = ("moefp8_abi_version", "moefp8_strerror", "moefp8_workspace_size", "moefp8_path", "moefp8_run",
-           "moefp8_run_noalloc", "moefp8_route", "moefp8_quantize_hidden")
+EXPORTS = ("moefp8_abi_version", "moefp8_strerror", "moefp8_workspace_size", "moefp8_path", "moefp8_output_passes",
+           "moefp8_run", "moefp8_run_noalloc", "moefp8_route", "moefp8_quantize_hidden")
 
 # MOEFP8_NOALLOC_SCRATCH_BYTES: static scratch of moefp8_run_noalloc
 NOALLOC_SCRATCH_BYTES = 64 << 20
@@ -74,8 +74,10 @@ class MoeFp8Args(ctypes.Structure):
     ]
 
 
-NUM_STAGE_EVENTS = 7
-STAGES = ("route", "permute", "gemm1", "activation", "gemm2", "combine")
+NUM_STAGE_EVENTS = 9
+# the last two stages run GEMM2 and the combine again for the second half of the output columns
+# when the per-pair output rows do not fit the workspace in one pass (empty otherwise)
+STAGES = ("route", "permute", "gemm1", "activation", "gemm2", "combine", "gemm2_b", "combine_b")
 
 
 class MoeFp8Error(RuntimeError):
@@ -107,6 +109,9 @@ def load(path: os.PathLike | None = None):
                                           ctypes.POINTER(ctypes.c_size_t)]
     lib.moefp8_path.restype = ctypes.c_int
     lib.moefp8_path.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]
+    lib.moefp8_output_passes.restype = ctypes.c_int
+    lib.moefp8_output_passes.argtypes = [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                         ctypes.c_int64]
     lib.moefp8_run.restype = ctypes.c_int
     lib.moefp8_run.argtypes = [ctypes.POINTER(MoeFp8Args), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
     lib.moefp8_run_noalloc.restype = ctypes.c_int

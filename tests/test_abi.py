@@ -63,7 +63,21 @@ def test_workspace_size(lib):
     small = _abi.workspace_size(lib, 16, 32, 7168, 2048)
     assert small < full
     pmax = 8192 * 8
-    assert full >= pmax * 7168 * 4          # fp32 per-pair GEMM2 rows
+    # fp32 per-pair GEMM2 rows for half the pairs' worth of all columns above 1 GiB of them: one
+    # pass over the columns while the call's pairs fit, two (half the columns each) beyond
+    passes = lib.moefp8_output_passes
+    assert full >= pmax * 3584 * 4
+    assert full <= 1.5e9
+    assert passes(8192, 32, 7168, 2048, 8587) == 1              # the benchmark's routing
+    assert passes(8192, 32, 7168, 2048, pmax // 2) == 1
+    assert passes(8192, 32, 7168, 2048, pmax // 2 + 1) == 2
+    assert passes(8192, 32, 7168, 2048, pmax) == 2
+    assert passes(4681, 32, 7168, 2048, 8 * 4681) == 1          # 4681 * 8 * 7168 * 4 B < 1 GiB: all rows
+    assert passes(4682, 32, 7168, 2048, 8 * 4682) == 2
+    assert passes(4682, 32, 384, 2048, 8 * 4682) == 1           # not the 128-row path (H % 256)
+    assert passes(64, 32, 7168, 2048, 512) == 1
+    assert passes(-1, 32, 7168, 2048, 0) == -2
+    assert passes(16, 32, 7168, 2048, -1) == -2
     assert _abi.workspace_size(lib, 0, 32, 7168, 2048) > 0
     out = ctypes.c_size_t()
     assert lib.moefp8_workspace_size(16, 32, 7000, 2048, ctypes.byref(out)) == -2   # H not a multiple of 128

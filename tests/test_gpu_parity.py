@@ -362,6 +362,63 @@ def test_rows_without_local_pair_overwrite_stale_output(T, E_local, H, I, shared
         assert torch.equal(rows, want)
 
 
+def _check_stale_rows(runner, ref32, nolocal, label):
+    """Two calls into an output buffer filled with NaN: output within the bar of the oracle and the
+    rows of tokens without a local pair exact zeros (every column of every row must be written)."""
+    for call in range(2):
+        runner.out.fill_(float("nan"))
+        out = runner()
+        torch.cuda.synchronize()
+        err = assert_close(out, ref32, f"{label}, call {call}")
+        assert torch.equal(out.cpu()[nolocal].float(), torch.zeros(int(nolocal.sum()), out.shape[1]))
+    return err
+
+
+def test_half_size_output_rows_at_full_size(full_weights):
+    """T = 4700 at H = 7168, I = 2048, E_local = 32: the workspace holds per-pair output rows for half
+    of T x 8 pairs (all of them would exceed 1 GiB); with this routing's pairs one pass over the
+    columns still serves them.  NaN-filled output buffer, two calls."""
+    from moe_fp8 import _abi
+    from moe_fp8.main import Runner
+    T = 4700
+    w_dev, w_cpu = full_weights
+    act = W.make_activations(W.Workload("half_rows", T, 4700), device="cpu")
+    ridx, _, _, _ = oracle_route(act[0], act[1])
+    P = int(((ridx >= 0) & (ridx < 32)).sum())
+    assert _abi.load().moefp8_output_passes(T, 32, 7168, 2048, P) == 1
+    ref32, _ = O.moe_forward(*act, *w_cpu, 0, W.RSF)
+    nolocal = torch.from_numpy(~np.any((ridx >= 0) & (ridx < 32), axis=1))
+    assert 0 < int(nolocal.sum()) < T
+    err = _check_stale_rows(Runner(*to_dev(act), *w_dev, 0, W.RSF), ref32, nolocal, "half-size O rows")
+    print(f"[half-size O rows] T={T} P={P} max_abs_err={err:.3e}", flush=True)
+
+
+def test_two_column_passes_when_pairs_outnumber_rows():
+    """T = 16400 at H = 2048, I = 128, E_local = 8: four tokens in five lean hard towards the 8 local
+    experts, so the call's pairs (~6 per such token) outnumber the workspace's per-pair output rows
+    (T x 8 / 2): GEMM2 and the combine run once per half of the output columns.  NaN-filled output
+    buffer, two calls, against the oracle."""
+    from moe_fp8 import _abi
+    from moe_fp8.main import Runner
+    T, E_local, H, I = 16400, 8, 2048, 128
+    weights = W.make_weights(E_local, H, I, device="cpu", seed=17)
+    args = W.make_inputs(W.Workload("two_pass", T, 16400), device="cpu", E_local=E_local, H=H, I=I,
+                         weights=weights)
+    logits = args[0].clone()
+    lean = torch.arange(T) % 5 != 0
+    logits[lean, :E_local] += 20.0
+    args = (logits,) + tuple(args[1:])
+    ridx, _, _, _ = oracle_route(args[0], args[1])
+    P = int(((ridx >= 0) & (ridx < E_local)).sum())
+    assert _abi.load().moefp8_path(T, E_local, H, I) == _abi.PATH_ROWS128
+    assert _abi.load().moefp8_output_passes(T, E_local, H, I, P) == 2, P
+    ref32, _ = O.moe_forward(*args)
+    nolocal = torch.from_numpy(~np.any((ridx >= 0) & (ridx < E_local), axis=1))
+    assert 0 < int(nolocal.sum()) < T
+    err = _check_stale_rows(Runner(*to_dev(args)), ref32, nolocal, "two column passes")
+    print(f"[two passes] T={T} P={P} max_abs_err={err:.3e}", flush=True)
+
+
 def test_deterministic_and_inputs_untouched():
     T, E_local, H, I = 700, 32, 256, 128
     wl = W.Workload("det", T, 5)
