@@ -155,15 +155,14 @@ int moefp8_output_passes(int64_t num_tokens, int32_t num_local_experts, int32_t 
  * (a hipStream_t; NULL = legacy default stream). */
 int moefp8_run(const moefp8_args* args, void* workspace, size_t workspace_bytes, void* stream);
 
-/* The operator without allocation.  No counterpart in the reference (whose run() allocates
- * through the torch allocator, main.py:202, 226-241): for callers that cannot allocate device
- * memory, such as code under HIP graph capture, tight serving loops and harnesses that forbid
- * hipMalloc.  Same arguments, work and results as moefp8_run, but the workspace is a static
- * device array of MOEFP8_NOALLOC_SCRATCH_BYTES (64 MiB) per device that loads the library, held
- * until the process ends; sizes whose moefp8_workspace_size() exceeds it return
- * MOEFP8_ERR_SCRATCH_LIMIT before any launch (it covers every T <= 64 of the operator's shapes,
- * H = 7168, I = 2048, any E_local, and T up to ~160 on the grouped path).  The call itself
- * allocates nothing.  Every call on a device shares that device's array: calls that overlap on
+/* The operator without allocation.  No counterpart in the reference: for callers that cannot
+ * allocate device memory, such as code under HIP graph capture, tight serving loops and harnesses
+ * that forbid hipMalloc.  Same arguments, work and results as moefp8_run, but the workspace is a
+ * static device array of MOEFP8_NOALLOC_SCRATCH_BYTES (64 MiB) per device that loads the library,
+ * held until the process ends; sizes whose moefp8_workspace_size() exceeds it return
+ * MOEFP8_ERR_SCRATCH_LIMIT before any launch (at H = 7168, I = 2048 it covers every T <= 226 for
+ * E_local 8, 32 or 256: the small-T and grouped paths and the 128-row path up to T = 226).  The
+ * call itself allocates nothing.  Every call on a device shares that device's array: calls that overlap on
  * one device (different streams, or other host threads) race and must be serialised by the
  * caller; calls on one stream are ordered by it.  Each call initialises what it reads. */
 #define MOEFP8_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)

@@ -1,8 +1,8 @@
 """The no-allocation entry point (moefp8_run_noalloc, static 64 MiB scratch per device) against
 moefp8_run on the same inputs, through the C ABI: bit-identical outputs and routing on two calls
-in a row, the second one smaller (T = 150 on the grouped 128-row path, then T = 16 on the
-small-T path), and again after the first size, so stale scratch contents from a larger call
-are never read."""
+in a row, the second one smaller (T = 150 on the 128-row path, then T = 16 on the small-T path),
+and again after the first size, so stale scratch contents from a larger call are never read.  At
+H = 7168, I = 2048 the scratch holds every T <= 226."""
 import ctypes
 
 import pytest
