@@ -120,6 +120,9 @@ def write_trace(d, workload, steps, warmup, cmd, out):
     return rows
 
 
+VGPR_FIELD_SCALE = 2
+
+
 def counter_means(dirs):
     """{kernel: {counter: mean per dispatch}} over every counter CSV under the given dirs, plus the
     dispatch's resources (grid, workgroup, LDS, VGPRs)."""
@@ -135,8 +138,11 @@ def counter_means(dirs):
                 if not k:
                     continue
                 vals[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
+                # rocprofv3's VGPR_Count is the descriptor's granule count x 4, while a gfx950
+                # wave64 allocates VGPRs in granules of 8: the allocation is twice the field
+                # (gemm1_big_kernel: field 112, compiler 217 VGPRs -> 224 allocated)
                 res.setdefault(k, dict(grid=int(r["Grid_Size"]), wg=int(r["Workgroup_Size"]),
-                                       lds=int(r["LDS_Block_Size"]), vgpr=int(r["VGPR_Count"]),
+                                       lds=int(r["LDS_Block_Size"]), vgpr=VGPR_FIELD_SCALE * int(r["VGPR_Count"]),
                                        agpr=int(r.get("Accum_VGPR_Count") or 0), sgpr=int(r["SGPR_Count"])))
     return {k: {c: statistics.fmean(v) for c, v in cs.items()} for k, cs in vals.items()}, res
 
@@ -167,7 +173,7 @@ def write_counters(dirs, workload, cmd, out, calibration=None):
     lines = [f"# Counters: moe_fp8 operator kernels, {workload}", ""] + [f"    {x}" for x in _stamp_lines(workload, cmd)]
     lines += ["", "Mean per dispatch over the run's dispatches of each kernel (rocprofv3 --pmc, one pass per "
               "counter group).", ""]
-    lines += ["| Kernel | grid x wg | LDS B | VGPR/AGPR | " + " | ".join(names) + " |",
+    lines += ["| Kernel | grid x wg | LDS B | VGPRs allocated / AGPR | " + " | ".join(names) + " |",
               "|---|---|---:|---|" + "---:|" * len(names)]
     for k in sorted(means):
         r = res[k]
