@@ -16,6 +16,11 @@ current kernels from a stale one.
 records come from runs one workload: one first call, N warmup calls, K timed calls, K calls
 with stage events, K warm back-to-back calls and the timed ``run()`` calls; every call but
 the warm ones follows a cache flush.
+
+Every figure is per operator call: the dispatches of one kernel within a call (the 128-row
+path launches GEMM2 and the combine once per output pass, the second launch returning at once
+when the call needs one pass) are summed, then averaged over calls.  A call starts at its
+routing kernel's dispatch.
 """
 from __future__ import annotations
 
@@ -79,10 +84,19 @@ def trace_calls(d):
     return calls
 
 
+def _per_call(call):
+    """{kernel: (dispatches, summed µs)} of one call."""
+    out = {}
+    for k, a, b in call:
+        n, t = out.get(k, (0, 0.0))
+        out[k] = (n + 1, t + (b - a) / 1e3)
+    return out
+
+
 def trace_summary(d, steps, warmup):
-    """Per kernel: mean duration (µs) over the cold timed calls (the timed and stage-event
-    passes), the mean over all calls, min and max; and the cold calls' first-start to last-end
-    span."""
+    """Per kernel: its summed duration per call (µs), averaged over the cold timed calls (the
+    timed and stage-event passes) and over all calls, with min and max over calls; and the cold
+    calls' first-start to last-end span."""
     calls = trace_calls(d)
     cold = calls[1 + warmup: 1 + warmup + 2 * steps]
     if not cold:
@@ -92,11 +106,15 @@ def trace_summary(d, steps, warmup):
         for k, _, _ in c:
             if k not in names:
                 names.append(k)
+    pc_all = [_per_call(c) for c in calls]
+    pc_cold = [_per_call(c) for c in cold]
     out = []
     for k in names:
-        allv = [(b - a) / 1e3 for c in calls for n, a, b in c if n == k]
-        coldv = [(b - a) / 1e3 for c in cold for n, a, b in c if n == k]
-        out.append(dict(kernel=k, calls=len(allv), cold_mean_us=statistics.fmean(coldv) if coldv else None,
+        allv = [pc[k][1] for pc in pc_all if k in pc]
+        coldv = [pc[k][1] for pc in pc_cold if k in pc]
+        per = max(pc[k][0] for pc in pc_all if k in pc)
+        out.append(dict(kernel=k, calls=len(allv), per_call=per,
+                        cold_mean_us=statistics.fmean(coldv) if coldv else None,
                         all_mean_us=statistics.fmean(allv), min_us=min(allv), max_us=max(allv)))
     out.sort(key=lambda r: -(r["cold_mean_us"] or 0.0))
     span = [(c[-1][2] - c[0][1]) / 1e3 for c in cold]
@@ -108,10 +126,13 @@ def write_trace(d, workload, steps, warmup, cmd, out):
     lines = [f"# Kernel trace: moe_fp8 operator, {workload}", ""] + [f"    {x}" for x in _stamp_lines(workload, cmd)]
     lines += ["", f"{n} operator calls traced; 'cold' = the {2 * steps} timed and stage-event calls (each after a "
               f"768 MiB read flush), the calls bench.py's figures come from.", "",
-              "| Kernel | Calls | Cold avg µs | All-call avg µs | Min µs | Max µs |", "|---|---:|---:|---:|---:|---:|"]
+              "Durations are per call: a kernel launched more than once per call (GEMM2 and the combine of the "
+              "128-row path, once per output pass) counts the sum of its launches.", "",
+              "| Kernel | Calls | Launches per call | Cold avg µs | All-call avg µs | Min µs | Max µs |",
+              "|---|---:|---:|---:|---:|---:|---:|"]
     for r in rows:
-        lines.append(f"| `{r['kernel']}` | {r['calls']} | {r['cold_mean_us']:.1f} | {r['all_mean_us']:.1f} | "
-                     f"{r['min_us']:.1f} | {r['max_us']:.1f} |")
+        lines.append(f"| `{r['kernel']}` | {r['calls']} | {r['per_call']} | {r['cold_mean_us']:.1f} | "
+                     f"{r['all_mean_us']:.1f} | {r['min_us']:.1f} | {r['max_us']:.1f} |")
     lines += ["", f"Cold call span (first kernel start to last kernel end): {span:.1f} µs", ""]
     for r in rows:
         lines.append(f"record kernel={r['kernel']} workload={workload} cold_us={r['cold_mean_us']:.2f} "
@@ -124,7 +145,8 @@ VGPR_FIELD_SCALE = 2
 
 
 def counter_means(dirs):
-    """{kernel: {counter: mean per dispatch}} over every counter CSV under the given dirs, plus the
+    """{kernel: {counter: mean per call}} over every counter CSV under the given dirs (each
+    counter summed over the kernel's dispatches in a call, then averaged over calls), plus the
     dispatch's resources (grid, workgroup, LDS, VGPRs)."""
     vals = defaultdict(lambda: defaultdict(list))
     res = {}
@@ -133,17 +155,32 @@ def counter_means(dirs):
         if not files:
             raise FileNotFoundError(f"no *counter_collection.csv under {d}")
         for f in files:
+            disp = {}
             for r in csv.DictReader(open(f)):
                 k = _kernel(r["Kernel_Name"])
                 if not k:
                     continue
-                vals[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
+                ent = disp.setdefault(int(r["Dispatch_Id"]), (k, {}))
+                ent[1][r["Counter_Name"]] = ent[1].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
                 # rocprofv3's VGPR_Count is the descriptor's granule count x 4, while a gfx950
                 # wave64 allocates VGPRs in granules of 8: the allocation is twice the field
                 # (gemm1_big_kernel: field 112, compiler 217 VGPRs -> 224 allocated)
                 res.setdefault(k, dict(grid=int(r["Grid_Size"]), wg=int(r["Workgroup_Size"]),
                                        lds=int(r["LDS_Block_Size"]), vgpr=VGPR_FIELD_SCALE * int(r["VGPR_Count"]),
                                        agpr=int(r.get("Accum_VGPR_Count") or 0), sgpr=int(r["SGPR_Count"])))
+            call = None
+            for _, (k, cs) in sorted(disp.items()):
+                if k == FIRST_KERNEL or call is None:
+                    for kk, sums in (call or {}).items():
+                        for c, v in sums.items():
+                            vals[kk][c].append(v)
+                    call = {}
+                sums = call.setdefault(k, {})
+                for c, v in cs.items():
+                    sums[c] = sums.get(c, 0.0) + v
+            for kk, sums in (call or {}).items():
+                for c, v in sums.items():
+                    vals[kk][c].append(v)
     return {k: {c: statistics.fmean(v) for c, v in cs.items()} for k, cs in vals.items()}, res
 
 
@@ -171,8 +208,8 @@ def write_counters(dirs, workload, cmd, out, calibration=None):
     means, res = counter_means(dirs)
     names = sorted({n for cs in means.values() for n in cs})
     lines = [f"# Counters: moe_fp8 operator kernels, {workload}", ""] + [f"    {x}" for x in _stamp_lines(workload, cmd)]
-    lines += ["", "Mean per dispatch over the run's dispatches of each kernel (rocprofv3 --pmc, one pass per "
-              "counter group).", ""]
+    lines += ["", "Mean per operator call over the run's calls, a kernel's dispatches within one call summed "
+              "(rocprofv3 --pmc, one pass per counter group).", ""]
     lines += ["| Kernel | grid x wg | LDS B | VGPRs allocated / AGPR | " + " | ".join(names) + " |",
               "|---|---|---:|---|" + "---:|" * len(names)]
     for k in sorted(means):
@@ -213,8 +250,9 @@ def write_traffic(fetch_dir, write_dir, kernel, workload, cmd, out):
     if kernel not in fm or kernel not in wm:
         raise KeyError(f"{kernel} not in the counter runs ({sorted(fm)})")
     fk, wk = fm[kernel]["FETCH_SIZE"], wm[kernel]["WRITE_SIZE"]
-    txt = "\n".join([f"# HBM traffic per dispatch of {kernel} on the {workload} workload",
-                     "# rocprofv3 FETCH_SIZE and WRITE_SIZE readings, KiB per dispatch (mean), one pass each:"]
+    txt = "\n".join([f"# HBM traffic per call of {kernel} on the {workload} workload",
+                     "# rocprofv3 FETCH_SIZE and WRITE_SIZE readings, KiB per operator call (the kernel's dispatches "
+                     "in a call summed, mean over calls), one pass each:"]
                     + [f"#   {x}" for x in _stamp_lines(workload, cmd)]
                     + [f"record kernel={kernel} workload={workload} fetch_kib={fk:.1f} write_kib={wk:.1f} "
                        f"source={source_hash()}"]) + "\n"

@@ -12,7 +12,7 @@ from moe_fp8 import build, profiling
 REPO = Path(__file__).resolve().parents[1]
 
 TRACE_FIELDS = ["Kernel_Name", "Start_Timestamp", "End_Timestamp"]
-COUNTER_FIELDS = ["Kernel_Name", "Counter_Name", "Counter_Value", "Grid_Size", "Workgroup_Size",
+COUNTER_FIELDS = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Grid_Size", "Workgroup_Size",
                   "LDS_Block_Size", "VGPR_Count", "Accum_VGPR_Count", "SGPR_Count"]
 
 
@@ -58,6 +58,19 @@ def test_kernel_names_and_call_split(tmp_path):
     assert span == pytest.approx(5 + 1 + 54.5 + 1 + 25)          # first start to last end of a cold call
 
 
+def test_kernel_launched_twice_per_call_is_summed(tmp_path):
+    # the 128-row path launches GEMM2 and the combine once per output pass; a one-pass call's
+    # second launches return at once and still count towards the call
+    calls = [[("route_kernel", 4000), ("gemm2_big_kernel", 400000 + 1000 * i), ("combine_kernel", 60000),
+              ("gemm2_big_kernel", 3000), ("combine_kernel", 2000)] for i in range(4)]
+    fake_trace(tmp_path, calls)
+    rows, _, n = profiling.trace_summary(tmp_path, steps=1, warmup=1)
+    by = {r["kernel"]: r for r in rows}
+    assert n == 4 and by["gemm2_big_kernel"]["per_call"] == 2 and by["gemm2_big_kernel"]["calls"] == 4
+    assert by["gemm2_big_kernel"]["cold_mean_us"] == pytest.approx((402 + 403) / 2 + 3)
+    assert by["combine_kernel"]["min_us"] == pytest.approx(62.0)
+
+
 def test_trace_record_roundtrip_and_staleness(tmp_path, monkeypatch):
     fake_trace(tmp_path / "kt", [[("route_kernel", 4000), ("gemm2_big_kernel", 400000)]] * 4)
     out = tmp_path / "moe_fp8_kernels_w.md"
@@ -83,17 +96,25 @@ def test_counters_derived_and_traffic(tmp_path, monkeypatch):
     res = {"Grid_Size": 131072, "Workgroup_Size": 512, "LDS_Block_Size": 150016, "VGPR_Count": 112,
            "Accum_VGPR_Count": 0, "SGPR_Count": 112}
     k = "void moefp8::gemm1_big_kernel(moefp8::Problem)"
-    sq = [dict(res, Kernel_Name=k, Counter_Name=n, Counter_Value=v) for n, v in
-          (("GRBM_GUI_ACTIVE", 8.0e6), ("SQ_VALU_MFMA_BUSY_CYCLES", 2.56e8), ("SQ_LDS_BANK_CONFLICT", 1.0e6),
-           ("SQ_LDS_IDX_ACTIVE", 4.0e6), ("SQ_INSTS_VALU", 9.0e7), ("SQ_INSTS_MFMA", 1.0e7))]
+    r0 = "void moefp8::route_kernel(int)"
+    k2 = "void moefp8::gemm2_big_kernel(moefp8::Problem)"
+    sq = [dict(res, Dispatch_Id=1, Kernel_Name=r0, Counter_Name="GRBM_GUI_ACTIVE", Counter_Value=1.0)]
+    sq += [dict(res, Dispatch_Id=2, Kernel_Name=k, Counter_Name=n, Counter_Value=v) for n, v in
+           (("GRBM_GUI_ACTIVE", 8.0e6), ("SQ_VALU_MFMA_BUSY_CYCLES", 2.56e8), ("SQ_LDS_BANK_CONFLICT", 1.0e6),
+            ("SQ_LDS_IDX_ACTIVE", 4.0e6), ("SQ_INSTS_VALU", 9.0e7), ("SQ_INSTS_MFMA", 1.0e7))]
     write_csv(tmp_path / "sq" / "run_counter_collection.csv", COUNTER_FIELDS, sq)
-    write_csv(tmp_path / "fetch" / "run_counter_collection.csv", COUNTER_FIELDS,
-              [dict(res, Kernel_Name=k, Counter_Name="FETCH_SIZE", Counter_Value=v) for v in (1000.0, 3000.0)])
+    # two calls: route, GEMM1, GEMM2 twice (its second launch nearly empty); rows in any order
+    fetch = [dict(res, Dispatch_Id=d, Kernel_Name=n, Counter_Name="FETCH_SIZE", Counter_Value=v) for d, n, v in
+             ((1, r0, 5.0), (2, k, 1000.0), (3, k2, 700.0), (4, k2, 14.0),
+              (5, r0, 5.0), (6, k, 3000.0), (7, k2, 900.0), (8, k2, 14.0))]
+    write_csv(tmp_path / "fetch" / "run_counter_collection.csv", COUNTER_FIELDS, fetch[::-1])
     write_csv(tmp_path / "write" / "run_counter_collection.csv", COUNTER_FIELDS,
-              [dict(res, Kernel_Name=k, Counter_Name="WRITE_SIZE", Counter_Value=500.0)])
+              [dict(res, Dispatch_Id=1, Kernel_Name=k, Counter_Name="WRITE_SIZE", Counter_Value=500.0)])
     means, resources = profiling.counter_means([tmp_path / "sq", tmp_path / "fetch"])
-    assert means["gemm1_big_kernel"]["FETCH_SIZE"] == pytest.approx(2000.0)   # mean per dispatch
+    assert means["gemm1_big_kernel"]["FETCH_SIZE"] == pytest.approx(2000.0)   # mean per call
+    assert means["gemm2_big_kernel"]["FETCH_SIZE"] == pytest.approx(814.0)    # both launches of a call
     assert resources["gemm1_big_kernel"]["wg"] == 512
+    assert resources["gemm1_big_kernel"]["vgpr"] == 224                        # the field x 2
     d = profiling.derived(means["gemm1_big_kernel"])
     # 2.56e8 busy SIMD-cycles over (8e6 / 8 XCDs) cycles x 256 CUs x 4 SIMDs
     assert d["mfma_busy"] == pytest.approx(0.25)
