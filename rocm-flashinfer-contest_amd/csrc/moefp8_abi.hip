@@ -502,11 +502,14 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
   mark(4);
   if (big) {
     // GEMM2 and the combine over the output columns: one pass, or two when the call's pairs
-    // outnumber O's rows (the kernels decide from the pair count; a pass with nothing to do exits)
+    // outnumber O's rows (the kernels decide from the pair count; a pass with nothing to do exits).
+    // O holds every pair a call can have whenever it has Pmax rows: no second pass is launched then
+    // (its two empty launches cost ~7 us per call, measured)
+    const int passes = L.o_rows >= L.pmax ? 1 : 2;
     for (int pass = 0; pass < 2; pass++) {
-      launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks2 * (H / 256)), (int)L.o_rows, pass, s);
+      if (pass < passes) launch_gemm2_big(pb, pl, ch, obuf, (int)(L.max_blocks2 * (H / 256)), (int)L.o_rows, pass, s);
       mark(5 + 2 * pass);
-      launch_combine_pass(pl, obuf, a->output, (int)T, H, (int)L.o_rows, pass, s);
+      if (pass < passes) launch_combine_pass(pl, obuf, a->output, (int)T, H, (int)L.o_rows, pass, s);
       mark(6 + 2 * pass);
     }
   } else {
