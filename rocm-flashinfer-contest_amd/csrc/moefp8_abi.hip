@@ -59,7 +59,7 @@ int large_rows_b(int64_t T, int E, int H, int I) { return large_big(T, E, H, I) 
 struct Layout {
   size_t topk_ids, topk_w, expert_offsets, active, mtile_offsets, info, perm_token, perm_w, tok_slot;
   size_t tok_a2, esig, mtiles, counters, c16, c16_scale, gbuf, obuf;
-  size_t canon_token, bcnt, ccnt, mblocks, mbgroup, two_term, queues, c_hi, c_lo16, c_scale;
+  size_t canon_token, bcnt, mblocks, mbgroup, two_term, queues, c_hi, c_lo16, c_scale;
   size_t g2_pair, g2_ctl, xrow;
   size_t total;
   int64_t pmax, max_mtiles, rows_cap, c_plane, max_blocks, max_blocks2, n_counters1, n_counters;
@@ -123,7 +123,6 @@ static Layout make_layout(int64_t T, int E_local, int H, int I) {
   L.max_blocks = (pmax + ra - 1) / ra + E_local + exact_blocks;
   L.canon_token = take((size_t)pmax * 4);
   L.bcnt = take((size_t)L.nblk * E_local * 3 * 4);
-  L.ccnt = take((size_t)L.nblk * E_local * 4);
   L.mblocks = take((size_t)L.max_blocks * 16);
   L.mbgroup = take((size_t)L.max_blocks * 8);
   L.two_term = take((size_t)L.max_blocks * 4);
@@ -449,7 +448,6 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
   pa.sqrt_i = sqrtf((float)I);
   pa.nblk = L.nblk;
   pa.bcnt = reinterpret_cast<int*>(ws + L.bcnt);
-  pa.ccnt = reinterpret_cast<int*>(ws + L.ccnt);
   pa.expert_offsets = const_cast<int*>(pl.expert_offsets);
   pa.mtile_offsets = const_cast<int*>(pl.mtile_offsets);
   pa.active = const_cast<int*>(pl.active);

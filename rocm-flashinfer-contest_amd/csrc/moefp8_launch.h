@@ -129,8 +129,7 @@ struct LargePermArgs {
   int T, E_local, offset;
   float sqrt_i;
   int nblk;
-  int* bcnt;            // [nblk][E_local * 3]
-  int* ccnt;            // [nblk][E_local]
+  int* bcnt;            // [nblk][E_local * 3] pairs per block and bucket
   int* expert_offsets;  // [E_local + 1]
   int* mtile_offsets;   // [E_local + 1]
   int* active;          // [E_local]

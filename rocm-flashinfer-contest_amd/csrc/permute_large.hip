@@ -1,11 +1,14 @@
-// Permutation of the (token, local expert) pairs for T > 64, in three launches over
-// blocks of 256 tokens (one token per thread):
+// Permutation of the (token, local expert) pairs for T > 64, in two launches over blocks of
+// 256 tokens (one token per thread):
 //
 //   count  per block, the number of pairs in each bucket (local expert, magnitude class)
-//   scan   one workgroup: bucket and expert offsets and the m-block table of the grouped
-//          GEMMs
-//   place  per block, each pair's rank inside its bucket in token order gives its row;
-//          the rank inside its expert alone gives its canonical row
+//   place  per block, from all blocks' counts (staged in LDS): every bucket's total and this
+//          block's prefix of it, hence the bucket and expert offsets; each pair's rank inside its
+//          bucket in token order then gives its row, the rank inside its expert alone its
+//          canonical row.  Block 0 also writes the offsets and the m-block table of the grouped
+//          GEMMs.  (A one-workgroup scan launch between the two took 5-7 us plus a launch
+//          boundary at T = 1024-8192; every block redoing the sums it needs costs it one round of
+//          loads.)
 //
 // Rows of an expert are grouped by magnitude class (class 0 first), each group in token
 // order, so pairs that need the exact-product or two-term paths share m-tiles instead of
@@ -21,7 +24,6 @@ namespace moefp8 {
 constexpr int kBlkTokens = 256;
 constexpr int kBlkWaves = kBlkTokens / kWave;
 constexpr int kClasses = 3;
-constexpr int kScanThreads = 1024;
 
 // 0: one f16 term of C is enough; 1: two terms; 2: two terms and exact GEMM1 products (GEMM2
 // may still take two terms for a class 0 block, from the C that GEMM1 writes).
@@ -106,6 +108,45 @@ __global__ __launch_bounds__(kBlkTokens) void perm_count_kernel(LargePermArgs a)
   for (int i = tid; i < E3; i += kBlkTokens) a.bcnt[(size_t)blockIdx.x * E3 + i] = cnt[i];
 }
 
+constexpr int kPlaceLdsInts = 6144;   // 24 KB of staged counts per round
+
+// tot[i] = bucket i's pairs over all blocks, pre[i] = over the blocks before `me` (E3 buckets),
+// from the per-block counts staged through LDS a chunk of blocks at a time (all of a chunk's
+// counts in one round of loads).  All threads of the block; ends with a barrier.
+__device__ void bucket_sums(const LargePermArgs& a, int me, int* tot, int* pre, int* stage) {
+  const int E3 = a.E_local * kClasses, nb = a.nblk, tid = threadIdx.x;
+  constexpr int kPer = kPlaceLdsInts / kBlkTokens;
+  static_assert(kPlaceLdsInts >= kEGlobal * kClasses, "a chunk holds at least one block");
+  const int chunk = min(nb, kPlaceLdsInts / E3);
+  for (int i = tid; i < E3; i += kBlkTokens) {
+    tot[i] = 0;
+    pre[i] = 0;
+  }
+  for (int b0 = 0; b0 < nb; b0 += chunk) {
+    const int n = min(chunk, nb - b0) * E3;
+    int v[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; q++) v[q] = a.bcnt[(size_t)b0 * E3 + min(tid + q * kBlkTokens, n - 1)];
+    // the previous chunk's readers are done
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kPer; q++)
+      if (tid + q * kBlkTokens < n) stage[tid + q * kBlkTokens] = v[q];
+    __syncthreads();
+    for (int i = tid; i < E3; i += kBlkTokens) {
+      int t = tot[i], pb = pre[i];
+      for (int b = 0; b * E3 < n; b++) {
+        const int c = stage[b * E3 + i];
+        t += c;
+        pb += b0 + b < me ? c : 0;
+      }
+      tot[i] = t;
+      pre[i] = pb;
+    }
+  }
+  __syncthreads();
+}
+
 // First index i in [0, n) with v[i] > x (v ascending).
 __device__ __forceinline__ int upper_bound(const int* v, int n, int x) {
   int lo = 0, hi = n;
@@ -117,86 +158,50 @@ __device__ __forceinline__ int upper_bound(const int* v, int n, int x) {
   return lo;
 }
 
-constexpr int kScanLdsInts = 12288;   // 48 KB of staged counts
-
-__global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a) {
-  __shared__ int tot[kEGlobal * kClasses];
-  __shared__ int scan_lds[kScanLdsInts];
-  __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], eb1[kEGlobal + 1];
-  const int E = a.E_local, E3 = E * kClasses, nb = a.nblk, tid = threadIdx.x, lane = lane_id();
-  if (tid < kUnitQueues) a.queues[tid * kQueueStride] = 0;
-  if (a.g2_ctl && tid < 2 * E) a.g2_ctl[tid] = 0;
-
-  // Per bucket: exclusive prefix of the raw counts over blocks (relative) and the total; per
-  // expert: the same over its three buckets (the canonical per-block base).  The counts are
-  // staged through LDS a chunk of blocks at a time with all threads loading, so that the
-  // sequential prefixes read LDS instead of waiting on one global load per block.
-  static_assert(kEGlobal * kClasses <= kScanThreads && kEGlobal <= kScanThreads / 2, "scan roles");
-  const int chunk = max(1, min(nb, kScanLdsInts / E3));
-  int run_b = 0, run_e = 0;
-  for (int b0 = 0; b0 < nb; b0 += chunk) {
-    const int nbc = min(chunk, nb - b0);
-    for (int i = tid; i < nbc * E3; i += kScanThreads) scan_lds[i] = a.bcnt[(size_t)b0 * E3 + i];
-    __syncthreads();
-    if (tid < E3) {
-      for (int b = 0; b < nbc; b++) {
-        const int c = scan_lds[b * E3 + tid];
-        a.bcnt[(size_t)(b0 + b) * E3 + tid] = run_b;
-        run_b += c;
-      }
-    }
-    const int e = tid - kScanThreads / 2;
-    if (e >= 0 && e < E) {
-      for (int b = 0; b < nbc; b++) {
-        const int* c = scan_lds + b * E3 + e * kClasses;
-        a.ccnt[(size_t)(b0 + b) * E + e] = run_e;
-        run_e += c[0] + c[1] + c[2];
-      }
-    }
-    // the chunk is read before the next one overwrites it
-    __syncthreads();
-  }
-  if (tid < E3) tot[tid] = run_b;
-  __syncthreads();
-  // expert offsets, 16-row m-tile offsets and m-block offsets, expert by expert: blocks of rows_a
-  // rows over an expert's class 0 and 1 rows (two-term C in the blocks that hold class 1 rows),
-  // then blocks of rows_b rows over its class 2 rows, or those folded into its last class 0/1
-  // block (folds_exact: 27 of 107 blocks at T = 8192 held <= 32 exact rows each, a quarter of the
-  // GEMMs' weight streams for 5% of the rows); both GEMMs run this one table (GEMM2 on
-  // separate class 0 and class 1 blocks had 11% more blocks, hence more weight streams, and was
-  // 4% slower at T = 8192).  An expert's blocks are consecutive, so the units that stream its
-  // weights run close together in time and share them through L2.
-  if (tid < kWave) {
-    int carry = 0, carry_mt = 0, carry_1 = 0, carry_act = 0;
-    for (int e0 = 0; e0 < E; e0 += kWave) {
-      const int e = e0 + lane;
-      const int n0 = e < E ? tot[kClasses * e] : 0, n1 = e < E ? tot[kClasses * e + 1] : 0;
-      const int n2 = e < E ? tot[kClasses * e + 2] : 0, n = n0 + n1 + n2;
-      const int mt = (n + 15) / 16;
-      const int ba = (n0 + n1 + a.rows_a - 1) / a.rows_a;
-      const int bx = folds_exact(a, n0 + n1, n2) ? 0 : (n2 + a.rows_b - 1) / a.rows_b;
-      const int b1 = ba + bx;
-      const int pn = wave_exclusive_sum(n), pmt = wave_exclusive_sum(mt);
-      const int p1 = wave_exclusive_sum(b1);
-      const uint64_t act = __ballot(n > 0);
-      if (e < E) {
-        eoff[e] = carry + pn;
-        emt[e] = carry_mt + pmt;
-        eb1[e] = carry_1 + p1;
+// Expert offsets, 16-row m-tile offsets and m-block offsets, expert by expert, from the bucket
+// totals (one wavefront): blocks of rows_a rows over an expert's class 0 and 1 rows (two-term C in
+// the blocks that hold class 1 rows), then blocks of rows_b rows over its class 2 rows, or those
+// folded into its last class 0/1 block (folds_exact: 27 of 107 blocks at T = 8192 held <= 32 exact
+// rows each, a quarter of the GEMMs' weight streams for 5% of the rows).  The grouped GEMMs run
+// this one table (GEMM2 on separate class 0 and class 1 blocks had 11% more blocks, hence more
+// weight streams, and was 4% slower at T = 8192; the 128-row GEMM2 builds its own from measured C).
+// An expert's blocks are consecutive, so the units that stream its weights run close together in
+// time and share them through L2.  With `write`, also the path's global tables.
+__device__ void expert_offsets(const LargePermArgs& a, const int* tot, int* eoff, int* emt, int* eb1, bool write) {
+  const int E = a.E_local, lane = lane_id();
+  int carry = 0, carry_mt = 0, carry_1 = 0, carry_act = 0;
+  for (int e0 = 0; e0 < E; e0 += kWave) {
+    const int e = e0 + lane;
+    const int n0 = e < E ? tot[kClasses * e] : 0, n1 = e < E ? tot[kClasses * e + 1] : 0;
+    const int n2 = e < E ? tot[kClasses * e + 2] : 0, n = n0 + n1 + n2;
+    const int mt = (n + 15) / 16;
+    const int ba = (n0 + n1 + a.rows_a - 1) / a.rows_a;
+    const int bx = folds_exact(a, n0 + n1, n2) ? 0 : (n2 + a.rows_b - 1) / a.rows_b;
+    const int b1 = ba + bx;
+    const int pn = wave_exclusive_sum(n), pmt = wave_exclusive_sum(mt);
+    const int p1 = wave_exclusive_sum(b1);
+    const uint64_t act = __ballot(n > 0);
+    if (e < E) {
+      eoff[e] = carry + pn;
+      emt[e] = carry_mt + pmt;
+      eb1[e] = carry_1 + p1;
+      if (write) {
         a.expert_offsets[e] = carry + pn;
         a.mtile_offsets[e] = carry_mt + pmt;
         a.xrow[e] = carry + pn + n0 + n1;
         if (n > 0) a.active[carry_act + lanes_below(act)] = e;
       }
-      carry += __builtin_amdgcn_readlane(pn + n, kWave - 1);
-      carry_mt += __builtin_amdgcn_readlane(pmt + mt, kWave - 1);
-      carry_1 += __builtin_amdgcn_readlane(p1 + b1, kWave - 1);
-      carry_act += (int)__popcll(act);
     }
-    if (lane == 0) {
-      eoff[E] = carry;
-      emt[E] = carry_mt;
-      eb1[E] = carry_1;
+    carry += __builtin_amdgcn_readlane(pn + n, kWave - 1);
+    carry_mt += __builtin_amdgcn_readlane(pmt + mt, kWave - 1);
+    carry_1 += __builtin_amdgcn_readlane(p1 + b1, kWave - 1);
+    carry_act += (int)__popcll(act);
+  }
+  if (lane == 0) {
+    eoff[E] = carry;
+    emt[E] = carry_mt;
+    eb1[E] = carry_1;
+    if (write) {
       a.expert_offsets[E] = carry;
       a.mtile_offsets[E] = carry_mt;
       a.info[0] = carry;                // P
@@ -204,20 +209,16 @@ __global__ __launch_bounds__(kScanThreads) void perm_scan_kernel(LargePermArgs a
       a.info[2] = carry_1;              // GEMM1 m-blocks
       a.info[3] = 1;                    // K-splits (small-T GEMMs only)
       a.info[4] = 1;
-      a.info[5] = carry_1;              // GEMM2 m-blocks: the same table
+      a.info[5] = carry_1;              // GEMM2 m-blocks of the grouped path: the same table
       a.info[6] = carry_mt;             // 16-row m-tiles
     }
   }
-  __syncthreads();
-  // absolute rows: bucket (e, c) starts after the expert's lower classes
-  for (int i = tid; i < nb * E3; i += kScanThreads) {
-    const int b3 = i % E3, e = b3 / kClasses, c = b3 - e * kClasses;
-    const int base = eoff[e] + (c > 0 ? tot[kClasses * e] : 0) + (c > 1 ? tot[kClasses * e + 1] : 0);
-    a.bcnt[i] += base;
-  }
-  for (int i = tid; i < nb * E; i += kScanThreads) a.ccnt[i] += eoff[i % E];
-  // m-block tables {expert, first row, rows, flags}
-  for (int g = tid; g < eb1[E]; g += kScanThreads) {
+}
+
+// The m-block table {expert, first row, rows, flags} and each block's expert group (all threads).
+__device__ void write_mblocks(const LargePermArgs& a, const int* tot, const int* eoff, const int* eb1) {
+  const int E = a.E_local;
+  for (int g = threadIdx.x; g < eb1[E]; g += blockDim.x) {
     const int e = upper_bound(eb1, E + 1, g) - 1, j = g - eb1[e];
     const int c0 = tot[kClasses * e], c01 = c0 + tot[kClasses * e + 1], n = eoff[e + 1] - eoff[e];
     const int ba = (c01 + a.rows_a - 1) / a.rows_a;
@@ -255,6 +256,10 @@ __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a)
   __shared__ unsigned long long bmask[kBlkWaves][kEGlobal * kClasses];
   __shared__ unsigned long long emask[kBlkWaves][kEGlobal];
   __shared__ float es[2 * kEGlobal];
+  // bucket totals and this block's prefix of them; expert, m-tile and m-block offsets
+  __shared__ int tot[kEGlobal * kClasses], pre[kEGlobal * kClasses];
+  __shared__ int eoff[kEGlobal + 1], emt[kEGlobal + 1], eb1[kEGlobal + 1];
+  __shared__ int stage[kPlaceLdsInts];
   const int E = a.E_local, E3 = E * kClasses, tid = threadIdx.x, wave = tid >> 6;
   const int t = blockIdx.x * kBlkTokens + tid;
   const bool in = t < a.T;
@@ -263,7 +268,16 @@ __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a)
   for (int i = tid; i < kBlkWaves * E3; i += kBlkTokens) bmask[i / E3][i % E3] = 0ull;
   for (int i = tid; i < kBlkWaves * E; i += kBlkTokens) emask[i / E][i % E] = 0ull;
   stage_esig(a, ts, es);
+  bucket_sums(a, blockIdx.x, tot, pre, stage);
+  const bool first = blockIdx.x == 0;
+  if (wave == 0) expert_offsets(a, tot, eoff, emt, eb1, first);
+  if (first) {
+    // the grouped GEMMs' unit queues and the 128-row GEMM2's row-table counters start at zero
+    if (tid < kUnitQueues) a.queues[tid * kQueueStride] = 0;
+    for (int i = tid; a.g2_ctl && i < 2 * E; i += kBlkTokens) a.g2_ctl[i] = 0;
+  }
   __syncthreads();
+  if (first) write_mblocks(a, tot, eoff, eb1);
   int bk[kTopK], ek[kTopK], rb[kTopK], re[kTopK];
 #pragma unroll
   for (int k = 0; k < kTopK; k++) {
@@ -272,13 +286,15 @@ __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a)
     rb[k] = 0;
     re[k] = 0;
   }
-  // the block's bucket and expert bases of every slot in one round of loads (slot 0's key
-  // where a slot is not local: in range, unused)
+  // the block's bases: bucket (e, c) starts after the expert's lower classes and this block's
+  // prefix of its own count; the expert's canonical rows after this block's prefix of its three
+  // buckets (slot 0's key where a slot is not local: in range, unused)
   int bb[kTopK], cb[kTopK];
 #pragma unroll
   for (int k = 0; k < kTopK; k++) {
-    bb[k] = a.bcnt[(size_t)blockIdx.x * E3 + max(bk[k], 0)];
-    cb[k] = a.ccnt[(size_t)blockIdx.x * E + max(ek[k], 0)];
+    const int b3 = max(bk[k], 0), e = b3 / kClasses, c = b3 - e * kClasses;
+    bb[k] = eoff[e] + (c > 0 ? tot[kClasses * e] : 0) + (c > 1 ? tot[kClasses * e + 1] : 0) + pre[b3];
+    cb[k] = eoff[e] + pre[kClasses * e] + pre[kClasses * e + 1] + pre[kClasses * e + 2];
   }
   wave_key_ranks(bk, rb, bmask[wave]);
   wave_key_ranks(ek, re, emask[wave]);
@@ -311,7 +327,6 @@ __global__ __launch_bounds__(kBlkTokens) void perm_place_kernel(LargePermArgs a)
 void launch_permute_large(const LargePermArgs& args, hipStream_t stream) {
   if (args.nblk <= 0) return;
   hipLaunchKernelGGL(perm_count_kernel, dim3(args.nblk), dim3(kBlkTokens), 0, stream, args);
-  hipLaunchKernelGGL(perm_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, args);
   hipLaunchKernelGGL(perm_place_kernel, dim3(args.nblk), dim3(kBlkTokens), 0, stream, args);
 }
 
