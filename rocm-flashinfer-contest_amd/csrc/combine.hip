@@ -16,30 +16,38 @@ constexpr int kCombineThreads = kCombineCols / 4;
 // its O rows.
 constexpr int kCombineSpareGrid = 256;
 
+// Token t's pair rows (tok_slot: ascending local expert, -1 past the last).
+__device__ __forceinline__ void load_slots(const int* __restrict__ tok_slot, int t, int (&slots)[kTopK]) {
+#pragma unroll
+  for (int k = 0; k < kTopK; k++) slots[k] = tok_slot[(size_t)t * kTopK + k];
+}
+
 // Token t's output columns [c, c + 4) (c inside [op.c0, op.c1)), from O rows [op.rows_cap][op.ocols]
 // holding the pass's columns from column 0.
-__device__ __forceinline__ void combine_quad(const int* __restrict__ tok_slot, const float* __restrict__ obuf,
+__device__ __forceinline__ void combine_quad(const int (&slots)[kTopK], const float* __restrict__ obuf,
                                              void* __restrict__ out, int t, int c, int H, int S, const OutPass& op,
                                              const void* shared, int shared_dt, int out_f32) {
   const int oc = c - op.c0;
-  int slots[kTopK];
-#pragma unroll
-  for (int k = 0; k < kTopK; k++) slots[k] = tok_slot[(size_t)t * kTopK + k];
   float4 acc = {0.f, 0.f, 0.f, 0.f};
   if (S == 1) {
-    float4 v[kTopK];
+    v4f v[kTopK];
 #pragma unroll
     for (int k = 0; k < kTopK; k++)
       v[k] = slots[k] >= 0
-                 ? *reinterpret_cast<const float4*>(obuf + (size_t)clamp_index(slots[k], op.rows_cap) * op.ocols + oc)
-                 : float4{0.f, 0.f, 0.f, 0.f};
+                 ? *reinterpret_cast<const v4f*>(obuf + (size_t)clamp_index(slots[k], op.rows_cap) * op.ocols + oc)
+                 : v4f{0.f, 0.f, 0.f, 0.f};
+    // every row's load issued before the first add (without this the compiler adds row 0 inside its
+    // load's branch and waits for it there, a second round trip for a token with several rows)
+    asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+    // slots past the token's last add +0.0, which changes no bit of a sum that starts at +0.0 (it is
+    // never -0.0)
 #pragma unroll
     for (int k = 0; k < kTopK; k++) {
-      if (slots[k] < 0) break;
-      acc.x += v[k].x;
-      acc.y += v[k].y;
-      acc.z += v[k].z;
-      acc.w += v[k].w;
+      const bool on = slots[k] >= 0;
+      acc.x += on ? v[k][0] : 0.f;
+      acc.y += on ? v[k][1] : 0.f;
+      acc.z += on ? v[k][2] : 0.f;
+      acc.w += on ? v[k][3] : 0.f;
     }
   } else {
     // K-split partials of each pair row, added split by split, then pair by pair
@@ -72,11 +80,18 @@ __global__ __launch_bounds__(kCombineThreads) void combine_kernel(const int* __r
                                                       void* __restrict__ out, int H, int o_rows, int pass,
                                                       const void* shared, int shared_dt, int out_f32,
                                                       int pair_rows) {
+  // the token's slots with the pair count and K-split, one round of loads (the slots do not depend
+  // on the pass)
+  int slots[kTopK];
+  load_slots(tok_slot, blockIdx.x, slots);
+  const int P = info[0], S = info[4];
+  asm volatile("" ::"s"(slots[0]), "s"(slots[1]), "s"(slots[2]), "s"(slots[3]), "s"(slots[4]), "s"(slots[5]),
+               "s"(slots[6]), "s"(slots[7]), "s"(P), "s"(S));
   OutPass op{0, H, H, pair_rows};
-  if (pass >= 0) op = out_pass(info[0], H, o_rows, pass, pair_rows);
+  if (pass >= 0) op = out_pass(P, H, o_rows, pass, pair_rows);
   const int c = op.c0 + blockIdx.y * kCombineCols + 4 * threadIdx.x;
   if (c >= op.c1) return;
-  combine_quad(tok_slot, obuf, out, blockIdx.x, c, H, info[4], op, shared, shared_dt, out_f32);
+  combine_quad(slots, obuf, out, blockIdx.x, c, H, S, op, shared, shared_dt, out_f32);
 }
 
 // The same over a fixed grid (items (token, 512 columns), tokens fastest), for an output pass that
@@ -92,7 +107,11 @@ __global__ __launch_bounds__(kCombineThreads) void combine_spare_kernel(const in
   for (int64_t item = blockIdx.x; item < (int64_t)T * n_chunks; item += gridDim.x) {
     const int t = (int)(item % T), chunk = (int)(item / T);
     const int c = op.c0 + chunk * kCombineCols + 4 * threadIdx.x;
-    if (c < op.c1) combine_quad(tok_slot, obuf, out, t, c, H, S, op, shared, shared_dt, out_f32);
+    if (c < op.c1) {
+      int slots[kTopK];
+      load_slots(tok_slot, t, slots);
+      combine_quad(slots, obuf, out, t, c, H, S, op, shared, shared_dt, out_f32);
+    }
   }
 }
 
