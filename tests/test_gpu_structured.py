@@ -9,6 +9,14 @@ predicts:
 * both, with every token routed to 8 local experts (forced logits), so that several large
   pair rows meet in each token's sum and cancel in some columns.
 
+and on structured weights:
+
+* flat_w2   -- an eighth of each expert's W2 rows hold +-448 codes under their block scales, so
+               their entries' rms is the blocks' maximum instead of the ~max/3 of Gaussian rows that
+               the one-term bound q is calibrated on (those output columns get ~3x the error of C's
+               one-term rounding), with log-normally amplified tokens (q up to and past 32) routed
+               to 8 local experts each, so that large pair rows meet and cancel in a token's sum.
+
 Bars as elsewhere: every element within atol 1e-2 / rtol 2e-2 of the oracle's fp32 output,
 an element that misses it re-evaluated for its token with fp64 accumulation."""
 import numpy as np
@@ -68,6 +76,52 @@ def build(kind, T, seed, w_cpu):
             x[t, ch] *= 100.0
     hs, hss = W.quantize_rows_1x128(x)
     return logits, bias, hs, hss
+
+
+@pytest.fixture(scope="module")
+def flat_w2_weights(weights):
+    """The module's weights with 1/8 of each expert's W2 rows at +-448 (e4m3fn codes 0x7e / 0xfe)."""
+    _, (w13, s13, w2, s2) = weights
+    g = torch.Generator().manual_seed(4711)
+    w2f = w2.clone()
+    codes = w2f.view(torch.uint8)
+    for e in range(E):
+        rows = torch.randperm(H, generator=g)[: H // 8]
+        signs = torch.randint(0, 2, (len(rows), I), generator=g, dtype=torch.uint8)
+        codes[e, rows] = 0x7E | (signs << 7)
+    w_cpu = (w13, s13, w2f, s2)
+    w_dev = tuple(x.to(DEV) for x in w_cpu)
+    torch.cuda.synchronize()
+    return w_dev, w_cpu
+
+
+def check(w_dev, w_cpu, act):
+    out = moe_fp8.run(*(a.to(DEV) for a in act), *w_dev, 0, W.RSF)
+    torch.cuda.synchronize()
+    ref32, _ = O.moe_forward(*act, *w_cpu, 0, W.RSF)
+    got = out.float().cpu()
+    print(f"  max |ref| {float(ref32.abs().max()):.1f}, max err {float((got - ref32).abs().max()):.4f}", flush=True)
+    miss = (got - ref32).abs() > ATOL + RTOL * ref32.abs()
+    bad = []
+    tokens = sorted({t for t, _ in torch.nonzero(miss).tolist()})
+    for t in tokens:
+        one = (act[0][t:t + 1], act[1], act[2][t:t + 1], act[3][:, t:t + 1].contiguous())
+        o64, _ = O.moe_forward(*one, *w_cpu, 0, W.RSF, accumulate=torch.float64)
+        for h in torch.nonzero(miss[t]).flatten().tolist():
+            exact = float(o64[0, h])
+            if abs(float(got[t, h]) - exact) > ATOL + RTOL * abs(exact):
+                bad.append((t, h, float(ref32[t, h]), exact, float(got[t, h])))
+    print(f"  {int(miss.sum())} elements miss the fp32 oracle's bar, {len(bad)} the fp64 value's", flush=True)
+    for b in bad[:10]:
+        print("   t=%d h=%d fp32 %.5f fp64 %.5f HIP %.5f" % b, flush=True)
+    assert not bad
+
+
+@pytest.mark.parametrize("T", [48, 100, 400])   # the small-T, grouped 16*MT-row and 128-row paths
+def test_structured_weights_flat_w2(flat_w2_weights, T):
+    print(f"[structured] flat_w2 T={T}", flush=True)
+    w_dev, w_cpu = flat_w2_weights
+    check(w_dev, w_cpu, build("amplified", T, 7100 + T, w_cpu))
 
 
 @pytest.mark.parametrize("kind", ["aligned", "aligned_block", "outliers", "both", "amplified"])
