@@ -35,17 +35,23 @@ struct DecodePlanScratch {
   float esig[2 * kEGlobal];             // weight-scale estimates of each local expert
 };
 
-// K-split of a decode GEMM: the largest S <= kDecMaxSplit whose units still fit one resident round
-// of the grid (n_mt * ncb * S <= slots) and whose partial rows fit (S * P <= rows_cap), and at
-// least ceil(kb / 64) (a unit holds the weight scales of its <= 64 K-blocks one per lane).  More
-// splits fill more of the grid at T = 1 or 4 but lengthen the reduction each group's last unit
-// does (measured at T = 1 / T = 4 with one and two pairs: S <= 4 31.6 / 38.9 us per call, S <= 8
-// 34.3 / 44.4, up to 20 splits 35.4 / 41.4 even with the counters on separate lines).
+// K-split of a decode GEMM.  Few m-tiles (their groups leave room for at least two splits within
+// `budget` units, two per CU): the most splits <= kDecFewSplit within the budget.  Otherwise the
+// largest S <= kDecMaxSplit whose units still fit one resident round of the grid
+// (n_mt * ncb * S <= slots).  Always S * P <= rows_cap (the partial rows) and S >= ceil(kb / 64) (a
+// unit holds the weight scales of its <= 64 K-blocks one per lane).  More splits fill more of the
+// grid but lengthen the reduction each group's last unit does; about two units per CU was the best
+// count for both GEMMs at T = 1 and 4 (one and two local pairs: GEMM1 S = 8 / 4, GEMM2 S = 4 / 2;
+// per call 29.6 -> 29.2 and 37.3 -> 36.5 us against S <= 4 everywhere; S <= 8 everywhere had cost
+// 34.3 / 44.4 against 31.6 / 38.9, up to 20 splits 35.4 / 41.4).
 constexpr int kDecMaxSplit = 4;
-__device__ __forceinline__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap) {
+constexpr int kDecFewSplit = 8;
+__device__ __forceinline__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap, int budget) {
   const int s_min = (kb + kWave - 1) / kWave;
+  const int per = n_mt * ncb;   // units per split
   int S = min(kb, kDecMaxSplit);
-  if (n_mt > 0 && ncb > 0) S = min(S, slots / (n_mt * ncb));
+  if (per > 0 && 2 * per <= budget) S = min(kb, min(kDecFewSplit, budget / per));
+  else if (per > 0) S = min(S, slots / per);
   if (P > 0) S = min(S, rows_cap / P);
   return max(S, s_min);
 }
@@ -123,8 +129,8 @@ __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, Dec
     if (lane == 0) {
       L.P = carry_p;
       L.n_mt = carry_mt;
-      L.S1 = pick_split(carry_mt, a.sp.ncb1, a.sp.kb1, a.sp.slots1, carry_p, a.sp.rows_cap1);
-      L.S2 = pick_split(carry_mt, a.sp.ncb2, a.sp.kb2, a.sp.slots2, carry_p, a.sp.rows_cap2);
+      L.S1 = pick_split(carry_mt, a.sp.ncb1, a.sp.kb1, a.sp.slots1, carry_p, a.sp.rows_cap1, a.sp.budget);
+      L.S2 = pick_split(carry_mt, a.sp.ncb2, a.sp.kb2, a.sp.slots2, carry_p, a.sp.rows_cap2, a.sp.budget);
       if (global) {
         a.expert_offsets[E] = carry_p;
         a.mtile_offsets[E] = carry_mt;

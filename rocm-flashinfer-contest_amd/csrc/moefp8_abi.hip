@@ -392,7 +392,8 @@ static int run_impl(const moefp8_args* a, void* workspace, size_t workspace_byte
     // small T: routing (+ scale estimates), GEMM1 (+ permutation plan, SwiGLU), GEMM2 (+ combine)
     const int groups = decode_unit_groups();
     const SplitPolicy sp = {decode_grid1(), 2 * I / (16 * groups), H / kBlock, (int)L.rows_cap,
-                            decode_grid2(), H / (16 * groups),     I / kBlock, (int)L.rows_cap};
+                            decode_grid2(), H / (16 * groups),     I / kBlock, (int)L.rows_cap,
+                            2 * num_compute_units()};
     pl.mtiles = reinterpret_cast<const int4*>(ws + L.mtiles);
     pl.counters = reinterpret_cast<int*>(ws + L.counters);
     pl.counters2 = pl.counters + L.n_counters1 * kCounterStride;

@@ -17,11 +17,11 @@ struct MagInputs {
   float* esig;     // [E, 2] rms estimates of W13 and W2 entries
 };
 
-// K-split choice of the small-T GEMMs: the largest S in {8, 4, 2, 1} with
-// m_tiles * ncb * S <= slots, S * P <= rows_cap and S <= kb.
+// Inputs of the small-T GEMMs' K-split choice (pick_split).
 struct SplitPolicy {
   int slots1, ncb1, kb1, rows_cap1;   // GEMM1: grid workgroups, column blocks per m-tile, K-blocks (H/128)
   int slots2, ncb2, kb2, rows_cap2;   // GEMM2: the same for H columns and I/128 K-blocks
+  int budget;                         // units that few m-tiles split into: two per CU
 };
 
 // Routing of every token (main.py:139-165): topk_ids [T,8] ascending, topk_w [T,8];
