@@ -120,7 +120,7 @@ constexpr int kQueueStride = 64;   // ints between queue counters: one 256-byte 
 constexpr int kCounterStride = 32;
 
 // Large-T path (T > 64).  Permutation arguments: pair counts per (block of 256 tokens,
-// bucket = local expert x magnitude class) and the outputs of the three launches.
+// bucket = local expert x magnitude class) and the outputs of its two launches.
 struct LargePermArgs {
   const int* topk_ids;
   const float* topk_w;
