@@ -30,12 +30,14 @@ __device__ __forceinline__ void combine_quad(const int (&slots)[kTopK], const fl
   const int oc = c - op.c0;
   float4 acc = {0.f, 0.f, 0.f, 0.f};
   if (S == 1) {
+    // O is read once, each row by whole lines (a wavefront's 64 lanes load 1 KB of it), so the loads
+    // carry the non-temporal hint (streamed through L2): 67.7 -> 61.5 us at T = 8192, measured
     v4f v[kTopK];
 #pragma unroll
     for (int k = 0; k < kTopK; k++)
-      v[k] = slots[k] >= 0
-                 ? *reinterpret_cast<const v4f*>(obuf + (size_t)clamp_index(slots[k], op.rows_cap) * op.ocols + oc)
-                 : v4f{0.f, 0.f, 0.f, 0.f};
+      v[k] = slots[k] >= 0 ? __builtin_nontemporal_load(reinterpret_cast<const v4f*>(
+                                 obuf + (size_t)clamp_index(slots[k], op.rows_cap) * op.ocols + oc))
+                           : v4f{0.f, 0.f, 0.f, 0.f};
     // every row's load issued before the first add (without this the compiler adds row 0 inside its
     // load's branch and waits for it there, a second round trip for a token with several rows)
     asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));

@@ -40,6 +40,15 @@ constexpr int kDec2BlocksPerCU = 5;          // GEMM2 too (<= 96 VGPRs: its per-
 constexpr int kDecDepth = 3;                 // K-blocks in flight per wavefront (register ring)
 static_assert(64 * kDecBlockWaves == kPlanThreads, "the GEMM1 workgroups build the plan");
 
+// One 16-byte chunk of a weight line on the staged paths.  Each weight byte is read once per
+// call and each 128-byte line by one load instruction (8 lanes), so the load carries the
+// non-temporal hint (streamed through L2): 5% less time per call at 16 tokens, measured.  The
+// per-step paths keep ordinary loads: their MFMA-layout loads split a line over two
+// instructions, and the hint evicts it in between (16% more time at 64 tokens, measured).
+__device__ __forceinline__ v4i load_w_line(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+}
+
 __device__ __forceinline__ v8i load_v8i(const uint8_t* p) {
   const v4i* q = reinterpret_cast<const v4i*>(p);
   const v4i x = q[0], y = q[1];
@@ -226,8 +235,8 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
       v4i B0[kDecDepth], B1[kDecDepth];
       auto load = [&](int d, int j) {
         const uint8_t* p = wsrc + (size_t)min(j, n - 1) * kBlock;
-        B0[d] = *reinterpret_cast<const v4i*>(p);
-        B1[d] = *reinterpret_cast<const v4i*>(p + (size_t)8 * H);
+        B0[d] = load_w_line(p);
+        B1[d] = load_w_line(p + (size_t)8 * H);
       };
 #pragma unroll
       for (int d = 0; d < kDecDepth; d++) load(d, d);
@@ -526,8 +535,8 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       v4i B0[kDecDepth], B1[kDecDepth];
       auto load = [&](int d, int j) {
         const uint8_t* p = wsrc + (size_t)min(j, n - 1) * kBlock;
-        B0[d] = *reinterpret_cast<const v4i*>(p);
-        B1[d] = *reinterpret_cast<const v4i*>(p + (size_t)8 * I);
+        B0[d] = load_w_line(p);
+        B1[d] = load_w_line(p + (size_t)8 * I);
       };
 #pragma unroll
       for (int d = 0; d < kDecDepth; d++) load(d, d);

@@ -111,6 +111,11 @@ __device__ __forceinline__ void dma_lds16_s(uint32_t voff, const void* sbase, ui
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase),
                "s"(lds_uniform) : "memory", "m0");
 }
+// The same with the non-temporal hint (streamed through L2), for lines read once per call.
+__device__ __forceinline__ void dma_lds16_s_nt(uint32_t voff, const void* sbase, uint32_t lds_uniform) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" : : "v"(voff), "s"(sbase),
+               "s"(lds_uniform) : "memory", "m0");
+}
 __device__ __forceinline__ void dma_lds4_s(uint32_t voff, const void* sbase, uint32_t lds_uniform) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase),
                "s"(lds_uniform) : "memory", "m0");
@@ -480,7 +485,13 @@ __device__ __forceinline__ TileSplit mixed_split(const RowMap& rm, int wm) {
 // than 64 rows, 2 for 33..64 rows and 1 for at most 32 (the short last blocks of an expert's
 // classes cost a quarter of the MFMA and VALU work of a full one).  kExact (blocks of at most 32
 // exact-product rows, NT = 1): the f16 MFMA on operands widened exactly, and C's lo term in f16.
-template <int NT, bool kExact>
+// kOnce: the block is its expert's only one, so each weight line is read once per call, by one
+// DMA instruction (8 lanes x 16 B), and its DMAs carry the non-temporal hint: 5% less GEMM1
+// time at 1024 tokens (about one block per expert), measured.  Experts with several blocks keep
+// ordinary DMAs, which let the blocks share the weights through L2 (the hint on every block cost
+// 20% at 8192 tokens, measured).  A template parameter, not a branch: the branch in the K loop
+// cost up to 4% on the other blocks, measured.
+template <int NT, bool kExact, bool kOnce>
 __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
                                                uint32_t ring_lds, const float2* sw_s, float (*amax_s)[kBgRows],
                                                int e, int row0, int rows, int cb, int* next_s, int n_units) {
@@ -522,8 +533,13 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
     const float* sbase = pb.hscale + (size_t)k * T;
 #pragma unroll
     for (int q = 0; q < 2; q++) dma_lds16_s(aoff[q], abase, st + (16 * wave + 8 * q) * 128);
+    if (kOnce) {
 #pragma unroll
-    for (int q = 0; q < 4; q++) dma_lds16_s(boff[q], bbase, st + kBgA + (32 * wave + 8 * q) * 128);
+      for (int q = 0; q < 4; q++) dma_lds16_s_nt(boff[q], bbase, st + kBgA + (32 * wave + 8 * q) * 128);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; q++) dma_lds16_s(boff[q], bbase, st + kBgA + (32 * wave + 8 * q) * 128);
+    }
     // wavefronts 2..7 repeat the row scales of 0 and 1 (same bytes), so that every wavefront
     // issues the same operations
     dma_lds4_s(soff, sbase, st + kBgA + kBgB + (wave & 1) * 256);
@@ -798,6 +814,7 @@ __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2
     const int mb = uniform(uc.x), cb = uniform(uc.y);
     const int4 blk = pl.mblocks[mb];
     const int e = uniform(blk.x), row0 = uniform(blk.y), rows = uniform(blk.z), flags = uniform(blk.w);
+    const bool once = uniform(pl.mbgroup[mb].y) == 1;   // the expert's only m-block
     // the previous unit's readers are done with the ring, amax_s and sw_s, and every thread has
     // read next_s
     __syncthreads();
@@ -829,11 +846,18 @@ __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2
       }
     } else {
 #define MOEFP8_G1_REG(NT, EXACT) \
-  gemm1_big_unit<NT, EXACT>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, &next_s, n_units)
-      if (flags & kFlagExactProducts) MOEFP8_G1_REG(1, true);
-      else if (rows <= 32) MOEFP8_G1_REG(1, false);
-      else if (rows <= 64) MOEFP8_G1_REG(2, false);
-      else MOEFP8_G1_REG(4, false);
+  if (once) gemm1_big_unit<NT, EXACT, true>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, &next_s, \
+                                            n_units); \
+  else gemm1_big_unit<NT, EXACT, false>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, &next_s, n_units)
+      if (flags & kFlagExactProducts) {
+        MOEFP8_G1_REG(1, true);
+      } else if (rows <= 32) {
+        MOEFP8_G1_REG(1, false);
+      } else if (rows <= 64) {
+        MOEFP8_G1_REG(2, false);
+      } else {
+        MOEFP8_G1_REG(4, false);
+      }
 #undef MOEFP8_G1_REG
     }
 #undef MOEFP8_G1_UNIT
