@@ -9,16 +9,23 @@
 // correctly rounded reciprocal multiply with an exact-residual correction, see div_by_scale).
 //
 // HBM-bound (2 + 1 bytes per value for bf16 in, plus 4 / 128 for the scales).  A workgroup
-// covers 16 tokens x 512 columns: each wavefront handles 4 tokens, a lane 8 consecutive values
+// covers 8 tokens x 512 columns: each wavefront handles 2 tokens, a lane 8 consecutive values
 // (one 16-byte bf16 load), so 16 lanes hold one 128-column block and its amax is a DPP
-// reduction inside the 16-lane row.  The 4 x 16 block scales go through LDS so that the
-// transposed [H/128, T] rows are written as 64-byte runs instead of 4-byte strided stores.
+// reduction inside the 16-lane row.  The 4 x 8 block scales go through LDS so that the
+// transposed [H/128, T] rows are written as 32-byte runs instead of 4-byte strided stores.
+// The grid is (512-column piece, token group): consecutive workgroups take consecutive pieces
+// of the same tokens, so the grid walks memory in order.  Measured at T = 8192: 32.4 us, against
+// 37.3 for 16 tokens with the token group fastest; 4 or 32 tokens 36.9 / 41.3; the same order as
+// a 1-D grid, whose workgroup index needs a division by the piece count, 35.6; non-temporal
+// loads and loads issued ahead of their bounds checks, no gain.
 #include "moefp8_device.h"
 #include "moefp8_launch.h"
 
 namespace moefp8 {
 
-constexpr int kQTokens = 16;        // tokens per workgroup
+constexpr int kQTokens = 8;         // tokens per workgroup
+constexpr int kQRows = kQTokens / 4;  // tokens per wavefront
+constexpr int kQMaxGroups = 65535;  // grid rows (token groups) per launch; more stride over them
 constexpr int kQCols = 512;         // columns per workgroup (4 blocks of 128)
 constexpr int kQThreads = 256;
 constexpr float kMinFastScale = 0x1p-100f;   // below it, reciprocal and quotient leave the normal range
@@ -72,58 +79,62 @@ __global__ __launch_bounds__(kQThreads) void quantize_hidden_kernel(const void* 
                                                                     float* __restrict__ scale) {
   __shared__ float sc_s[kQCols / kBlock][kQTokens];
   const int wave = threadIdx.x >> 6, lane = lane_id();
-  const int t0 = blockIdx.x * kQTokens, c0 = blockIdx.y * kQCols;
+  const int c0 = blockIdx.x * kQCols;
   const int col = c0 + 8 * lane;                 // this lane's 8 columns
   const bool in_cols = col < H;                  // H is a multiple of 128: whole 16-lane rows
-  const int kb = col / kBlock;                   // block of those columns
-  float v[4][8];
+  for (int t0 = blockIdx.y * kQTokens; t0 < T; t0 += gridDim.y * kQTokens) {
+    float v[kQRows][8];
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int t = t0 + 4 * wave + r;
-    if (t < T && in_cols) load8<kDt>(x, (size_t)t * H + col, v[r]);
-    else
+    for (int r = 0; r < kQRows; r++) {
+      const int t = t0 + kQRows * wave + r;
+      if (t < T && in_cols) load8<kDt>(x, (size_t)t * H + col, v[r]);
+      else
 #pragma unroll
-      for (int j = 0; j < 8; j++) v[r][j] = 0.f;
-  }
-#pragma unroll
-  for (int r = 0; r < 4; r++) {
-    const int t = t0 + 4 * wave + r;
-    float a = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; j++) a = fmaxf(a, fabsf(v[r][j]));
-    const float amax = row16_max(a);
-    const float s = amax > 0.f ? amax / 448.0f : 1.0f;
-    uint32_t lo = 0, hi = 0;
-    if (s >= kMinFastScale) {
-      const float y = recip_rn(s);
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        lo |= f32_to_e4m3(div_by_scale(v[r][j], s, y)) << (8 * j);
-        hi |= f32_to_e4m3(div_by_scale(v[r][4 + j], s, y)) << (8 * j);
-      }
-    } else {
-      // scales near the bottom of the fp32 range (1/s would overflow): IEEE division
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        lo |= f32_to_e4m3(v[r][j] / s) << (8 * j);
-        hi |= f32_to_e4m3(v[r][4 + j] / s) << (8 * j);
-      }
+        for (int j = 0; j < 8; j++) v[r][j] = 0.f;
     }
-    if (t < T && in_cols) *reinterpret_cast<uint2*>(q + (size_t)t * H + col) = uint2{lo, hi};
-    if ((lane & 15) == 0) sc_s[lane >> 4][4 * wave + r] = s;
-  }
-  __syncthreads();
-  // scale rows: 4 blocks x 16 consecutive tokens
-  if (threadIdx.x < (kQCols / kBlock) * kQTokens) {
-    const int b = threadIdx.x / kQTokens, i = threadIdx.x % kQTokens;
-    const int kbw = c0 / kBlock + b, t = t0 + i;
-    if (t < T && kbw < H / kBlock) scale[(size_t)kbw * T + t] = sc_s[b][i];
+#pragma unroll
+    for (int r = 0; r < kQRows; r++) {
+      const int t = t0 + kQRows * wave + r;
+      float a = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; j++) a = fmaxf(a, fabsf(v[r][j]));
+      const float amax = row16_max(a);
+      const float s = amax > 0.f ? amax / 448.0f : 1.0f;
+      uint32_t lo = 0, hi = 0;
+      if (s >= kMinFastScale) {
+        const float y = recip_rn(s);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          lo |= f32_to_e4m3(div_by_scale(v[r][j], s, y)) << (8 * j);
+          hi |= f32_to_e4m3(div_by_scale(v[r][4 + j], s, y)) << (8 * j);
+        }
+      } else {
+        // scales near the bottom of the fp32 range (1/s would overflow): IEEE division
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          lo |= f32_to_e4m3(v[r][j] / s) << (8 * j);
+          hi |= f32_to_e4m3(v[r][4 + j] / s) << (8 * j);
+        }
+      }
+      if (t < T && in_cols) *reinterpret_cast<uint2*>(q + (size_t)t * H + col) = uint2{lo, hi};
+      if ((lane & 15) == 0) sc_s[lane >> 4][kQRows * wave + r] = s;
+    }
+    __syncthreads();
+    // scale rows: 4 blocks x 8 consecutive tokens
+    if (threadIdx.x < (kQCols / kBlock) * kQTokens) {
+      const int b = threadIdx.x / kQTokens, i = threadIdx.x % kQTokens;
+      const int kbw = c0 / kBlock + b, t = t0 + i;
+      if (t < T && kbw < H / kBlock) scale[(size_t)kbw * T + t] = sc_s[b][i];
+    }
+    // the scales are read before the next group writes them
+    __syncthreads();
   }
 }
 
 void launch_quantize_hidden(const void* x, int x_dt, int64_t T, int H, uint8_t* q, float* scale, hipStream_t stream) {
   if (T <= 0) return;
-  const dim3 grid((unsigned)((T + kQTokens - 1) / kQTokens), (unsigned)((H + kQCols - 1) / kQCols));
+  const int64_t groups = (T + kQTokens - 1) / kQTokens;
+  const dim3 grid((unsigned)((H + kQCols - 1) / kQCols), (unsigned)(groups < kQMaxGroups ? groups : kQMaxGroups));
   if (x_dt == 1)
     hipLaunchKernelGGL(quantize_hidden_kernel<1>, grid, dim3(kQThreads), 0, stream, x, (int)T, H, q, scale);
   else

@@ -139,6 +139,17 @@ def test_route_rejects_bad_arguments(lib):
     assert f(0x1008, 0, 0x2000, 1, 4, 2.5, 0x3000, 0x4000, None) == -4   # fp32 logits: 16-byte aligned
 
 
+def test_quantize_rejects_bad_arguments(lib):
+    f = lib.moefp8_quantize_hidden
+    assert f(0x1000, 1, -1, 7168, 0x2000, 0x3000, None) == -2
+    assert f(0x1000, 1, (1 << 24) + 1, 128, 0x2000, 0x3000, None) == -2
+    assert f(0x1000, 1, 16, 100, 0x2000, 0x3000, None) == -2
+    assert f(0x1000, 2, 16, 7168, 0x2000, 0x3000, None) == -3
+    assert f(0x1000, 1, 0, 7168, 0x2000, 0x3000, None) == 0
+    assert f(None, 1, 16, 7168, 0x2000, 0x3000, None) == -1
+    assert f(0x1008, 1, 16, 7168, 0x2000, 0x3000, None) == -4             # x: 16-byte aligned
+
+
 def test_python_entry_point_fails_loudly_without_device_tensors(lib):
     import torch
     import moe_fp8

@@ -151,6 +151,21 @@ def test_quantize_full_size_t8192():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("T,H", [(65535 * 8 + 37, 128), (65535 * 8 * 2 + 8, 384)])
+def test_quantize_more_token_groups_than_grid_rows(T, H):
+    """A launch holds at most 65535 groups of 8 tokens: later groups are reached by striding, the
+    last one partial."""
+    import moe_fp8
+    print(f"[quantize] T={T} H={H} bf16 (strided token groups)", flush=True)
+    x = sample(T, H, 13, torch.bfloat16)
+    q, scale = moe_fp8.quantize_hidden(x.to(DEV))
+    torch.cuda.synchronize()
+    want_codes, want_scale = O.quantize_hidden(x)
+    assert np.array_equal(scale.cpu().numpy(), want_scale)
+    assert np.array_equal(q.view(torch.uint8).cpu().numpy(), want_codes)
+
+
+@pytest.mark.gpu
 def test_quantize_feeds_run():
     """The quantizer's output is the operator's input: run() on it equals run() on the
     oracle's quantization of the same activations, bit for bit."""
