@@ -126,6 +126,15 @@ __device__ __forceinline__ void barrier_lds() {
   asm volatile("" ::: "memory");
 }
 #define MOEFP8_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(" #n ")" ::: "memory")
+// The same for a wave-uniform count n in [2, 7] (the count is an immediate of the instruction).
+__device__ __forceinline__ void wait_vmcnt_2to7(int n) {
+  if (n <= 2) MOEFP8_WAIT_VMCNT(2);
+  else if (n == 3) MOEFP8_WAIT_VMCNT(3);
+  else if (n == 4) MOEFP8_WAIT_VMCNT(4);
+  else if (n == 5) MOEFP8_WAIT_VMCNT(5);
+  else if (n == 6) MOEFP8_WAIT_VMCNT(6);
+  else MOEFP8_WAIT_VMCNT(7);
+}
 
 // Wave-uniform read of kernel-constant data through the constant address space, so the
 // compiler can use a scalar load (counted by lgkmcnt, not by the vmcnt pipeline above).
@@ -493,7 +502,8 @@ __device__ __forceinline__ TileSplit mixed_split(const RowMap& rm, int wm) {
 // cost up to 4% on the other blocks, measured.
 template <int NT, bool kExact, bool kOnce>
 __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
-                                               uint32_t ring_lds, const float2* sw_s, float (*amax_s)[kBgRows],
+                                               uint32_t ring_lds, uint32_t sink_lds, const float2* sw_s,
+                                               float (*amax_s)[kBgRows],
                                                int e, int row0, int rows, int cb, int* next_s, int n_units) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
   static_assert(!kExact || NT == 1, "exact-product blocks hold at most 32 rows");
@@ -523,7 +533,7 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
     boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ slot_key8(R)) * 16);
   }
   const uint32_t soff =
-      4u * (uint32_t)clamp_index(pl.perm_token[row0 + min(64 * (wave & 1) + lane, rows - 1)], T);
+      wave < 2 ? 4u * (uint32_t)clamp_index(pl.perm_token[row0 + min(64 * (wave & 1) + lane, rows - 1)], T) : 0u;
   const uint8_t* wbase = pb.w13 + (size_t)e * 2 * I * H;
   auto issue = [&](int j) {
     const int k = min(j, KB - 1);
@@ -540,9 +550,10 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
 #pragma unroll
       for (int q = 0; q < 4; q++) dma_lds16_s(boff[q], bbase, st + kBgA + (32 * wave + 8 * q) * 128);
     }
-    // wavefronts 2..7 repeat the row scales of 0 and 1 (same bytes), so that every wavefront
-    // issues the same operations
-    dma_lds4_s(soff, sbase, st + kBgA + kBgB + (wave & 1) * 256);
+    // every wavefront issues the same operations: wavefronts 0 and 1 DMA the row scales of rows
+    // 64 w + lane, 2..7 one 4-byte word (one line, all lanes) into a sink: GEMM1 -3 / -4 to -8 µs
+    // at T = 1024 / 8192 against all eight DMAing the 64 scattered scales of 0 and 1 (measured)
+    dma_lds4_s(soff, sbase, wave < 2 ? st + kBgA + kBgB + (wave & 1) * 256 : sink_lds);
   };
 
   // the table and scale loads of the unit are complete: only DMAs count from here
@@ -649,7 +660,8 @@ __device__ __forceinline__ void gemm1_big_unit(const Problem& pb, const Plan& pl
 // worse in this general form, LDS reads no longer hoisted ahead of the MFMAs, ~10% slower.)
 template <int NF, int NX>
 __device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Plan& pl, const CHalf8& ch, uint8_t* ring,
-                                               uint32_t ring_lds, const float2* sw_s, float (*amax_s)[kBgRows],
+                                               uint32_t ring_lds, uint32_t sink_lds, const float2* sw_s,
+                                               float (*amax_s)[kBgRows],
                                                int e, const RowMap& rm, int cb, int tf0, int tx0, int* next_s,
                                                int n_units) {
   constexpr int NT = NF + NX;
@@ -680,7 +692,7 @@ __device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Pl
     const int wrow = (n < 2 ? 0 : I) + cb * kBlock + 32 * g + 16 * (n & 1) + rr;
     boff[q] = (uint32_t)wrow * (uint32_t)H + (uint32_t)((dslot ^ slot_key8(R)) * 16);
   }
-  const uint32_t soff = 4u * (uint32_t)clamp_index(pl.perm_token[rm.src(64 * (wave & 1) + lane)], T);
+  const uint32_t soff = wave < 2 ? 4u * (uint32_t)clamp_index(pl.perm_token[rm.src(64 * (wave & 1) + lane)], T) : 0u;
   const uint8_t* wbase = pb.w13 + (size_t)e * 2 * I * H;
   auto issue = [&](int j) {
     const int k = min(j, KB - 1);
@@ -692,9 +704,10 @@ __device__ __forceinline__ void gemm1_big_mixed_unit(const Problem& pb, const Pl
     for (int q = 0; q < 2; q++) dma_lds16_s(aoff[q], abase, st + (16 * wave + 8 * q) * 128);
 #pragma unroll
     for (int q = 0; q < 4; q++) dma_lds16_s(boff[q], bbase, st + kBgA + (32 * wave + 8 * q) * 128);
-    // wavefronts 2..7 repeat the row scales of 0 and 1 (same bytes), so that every wavefront
-    // issues the same operations
-    dma_lds4_s(soff, sbase, st + kBgA + kBgB + (wave & 1) * 256);
+    // every wavefront issues the same operations: wavefronts 0 and 1 DMA the row scales of rows
+    // 64 w + lane, 2..7 one 4-byte word (one line, all lanes) into a sink: GEMM1 -3 / -4 to -8 µs
+    // at T = 1024 / 8192 against all eight DMAing the 64 scattered scales of 0 and 1 (measured)
+    dma_lds4_s(soff, sbase, wave < 2 ? st + kBgA + kBgB + (wave & 1) * 256 : sink_lds);
   };
 
   // the table and scale loads of the unit are complete: only DMAs count from here
@@ -804,6 +817,9 @@ __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2
   __shared__ __attribute__((aligned(16))) float2 sw_s[kBigMaxKB];
   __shared__ float amax_s[4][kBgRows];
   const int H = pb.H, I = pb.I, KB = H / kBlock, NCB = I / kBlock;
+  // where wavefronts 2..7 put their row-scale DMA (never read)
+  __shared__ __attribute__((aligned(16))) uint32_t dma_sink[64];
+  const uint32_t sink_lds = uniform((int)lds_addr(dma_sink));
   __shared__ int next_s;
   const uint32_t ring_lds = uniform((int)lds_addr(ring));
   const int n_units = pl.info[2] * NCB;
@@ -829,7 +845,8 @@ __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2
     const RowMap rm = row_map(row0, rows, flags);
     const int wm = wave_index() & 1;
 #define MOEFP8_G1_UNIT(NF, NX, TF0, TX0) \
-  gemm1_big_mixed_unit<NF, NX>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, rm, cb, TF0, TX0, &next_s, n_units)
+  gemm1_big_mixed_unit<NF, NX>(pb, pl, ch, ring, ring_lds, sink_lds, sw_s, amax_s, e, rm, cb, TF0, TX0, &next_s, \
+                               n_units)
     if (flags & kFlagMixed) {
       const TileSplit ts = mixed_split(rm, wm);
       const int nf = uniform(ts.nf), tf0 = uniform(ts.tf0), tx0 = uniform(ts.tx0);
@@ -846,9 +863,10 @@ __global__ __launch_bounds__(kBgThreads, 1) __attribute__((amdgpu_waves_per_eu(2
       }
     } else {
 #define MOEFP8_G1_REG(NT, EXACT) \
-  if (once) gemm1_big_unit<NT, EXACT, true>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, &next_s, \
-                                            n_units); \
-  else gemm1_big_unit<NT, EXACT, false>(pb, pl, ch, ring, ring_lds, sw_s, amax_s, e, row0, rows, cb, &next_s, n_units)
+  if (once) gemm1_big_unit<NT, EXACT, true>(pb, pl, ch, ring, ring_lds, sink_lds, sw_s, amax_s, e, row0, rows, cb, \
+                                            &next_s, n_units); \
+  else gemm1_big_unit<NT, EXACT, false>(pb, pl, ch, ring, ring_lds, sink_lds, sw_s, amax_s, e, row0, rows, cb, \
+                                        &next_s, n_units)
       if (flags & kFlagExactProducts) {
         MOEFP8_G1_REG(1, true);
       } else if (rows <= 32) {
@@ -1119,19 +1137,33 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
                                                const G2Rows& rm, int hc, float* __restrict__ obuf, int ocol0,
                                                int ocols, int orows, int* queues, int* next_s, int n_units) {
   static_assert(NT == 1 || NT == 2 || NT == 4, "m-tiles per wavefront");
-  constexpr int kOps = kTwo ? 7 : 5;   // DMAs per wavefront and stage: hi 2, lo 2, W2 2, row scales 1
   const int H = pb.H, I = pb.I, KB = I / kBlock, KS = I / 64;
   // lane-dependent addresses are formed per unit (hoisted out of the unit loop, some of them spill)
   int lane = lane_id();
   asm volatile("" : "+v"(lane));
   const int wave = wave_index(), lr = lane & 15, kg = lane >> 4;
   const int wm = wave & 1, wn = wave >> 1;
-  // DMA sources (per-lane byte offsets): hi and lo rows 16w + 8q + (lane / 8), 8 slots per row;
-  // W2 rows 32w + 16q + (lane / 4), 4 slots per row; row scales 64 (w % 2) + lane
-  uint32_t hoff[2], woff[2];
+  // DMA roles.  A stage waits for its slowest wavefront, and every DMA instruction costs the
+  // wavefront that issues it, so each wavefront issues only DMAs of rows the block computes, and
+  // the row scales go with the odd 64-K stage of a 128-K block only (the stage that applies them):
+  // GEMM2 114 -> 112, 229 -> 217 and 410 -> 389 µs at T = 1024 / 5000 / 8192 against every
+  // wavefront DMAing 16 rows of hi (and lo) and the scales each stage (measured).
+  //   hi / lo rows, in groups of 8 (one DMA each): NT = 4, groups 2w and 2w + 1; NT = 2 (rows <=
+  //   64), group w; NT = 1 (rows <= 32), groups 0..3 by waves 2..5.
+  //   W2 rows 32w + 16q + (lane / 4), 4 slots per row, 2 DMAs per wavefront.
+  //   row scales: NT = 4, rows 64 (w % 2) + lane by waves 0 and 1; NT = 2 / 1, rows 0..63 by
+  //   wave 0 / 6.
+  constexpr int kHiPer = NT == 4 ? 2 : 1;
+  const int hi0 = NT == 4 ? 2 * wave : NT == 2 ? wave : max(wave - 2, 0);   // first group carried
+  const bool hcar = NT != 1 || (wave >= 2 && wave < 6);
+  const bool scar = NT == 4 ? wave < 2 : NT == 2 ? wave == 0 : wave == 6;
+  const int sslot = NT == 4 ? (wave & 1) : 0;
+  const int n_even = 2 + (hcar ? kHiPer * (kTwo ? 2 : 1) : 0);   // DMAs of an even stage
+  const int n_odd = n_even + (scar ? 1 : 0);                      // of an odd one
+  uint32_t hoff[kHiPer], woff[2];
 #pragma unroll
-  for (int q = 0; q < 2; q++) {
-    const int r = 16 * wave + 8 * q + (lane >> 3);
+  for (int q = 0; q < kHiPer; q++) {
+    const int r = 8 * (hi0 + q) + (lane >> 3);
     hoff[q] = (uint32_t)clamp_index(rm.src(r), pl.pair_rows) * (uint32_t)(2 * I) +
               (uint32_t)((((lane & 7) ^ slot_key8(r))) * 16);
   }
@@ -1140,23 +1172,25 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
     const int R = 32 * wave + 16 * q + (lane >> 2);
     woff[q] = (uint32_t)(hc * kB2Cols + R) * (uint32_t)I + (uint32_t)((((lane & 3) ^ bg_key4(R))) * 16);
   }
-  const uint32_t soff = 4u * (uint32_t)(clamp_index(rm.src(64 * (wave & 1) + lane), pl.pair_rows) * KB);
+  const uint32_t soff = 4u * (uint32_t)(clamp_index(rm.src(64 * sslot + lane), pl.pair_rows) * KB);
   const uint8_t* wbase = pb.w2 + (size_t)e * H * I;
   auto issue = [&](int j) {
     const int k = min(j, KS - 1);
     const uint32_t st = ring_lds + (uint32_t)((j % kB2Stages) * kB2Stage);
     const uint8_t* hbase = reinterpret_cast<const uint8_t*>(ch.hi) + (size_t)k * 128;
+    if (hcar) {
 #pragma unroll
-    for (int q = 0; q < 2; q++) dma_lds16_s(hoff[q], hbase, st + (16 * wave + 8 * q) * 128);
-    if (kTwo) {
-      const uint8_t* lbase = reinterpret_cast<const uint8_t*>(ch.lo16) + (size_t)k * 128;
+      for (int q = 0; q < kHiPer; q++) dma_lds16_s(hoff[q], hbase, st + 8 * (hi0 + q) * 128);
+      if (kTwo) {
+        const uint8_t* lbase = reinterpret_cast<const uint8_t*>(ch.lo16) + (size_t)k * 128;
 #pragma unroll
-      for (int q = 0; q < 2; q++) dma_lds16_s(hoff[q], lbase, st + kB2Hi + (16 * wave + 8 * q) * 128);
+        for (int q = 0; q < kHiPer; q++) dma_lds16_s(hoff[q], lbase, st + kB2Hi + 8 * (hi0 + q) * 128);
+      }
     }
 #pragma unroll
     for (int q = 0; q < 2; q++)
       dma_lds16_s(woff[q], wbase + (size_t)k * 64, st + kB2Hi + kB2Lo + (32 * wave + 16 * q) * 64);
-    dma_lds4_s(soff, ch.scale + k / 2, st + kB2Hi + kB2Lo + kB2W + (wave & 1) * 256);
+    if (scar && (j & 1)) dma_lds4_s(soff, ch.scale + k / 2, st + kB2Hi + kB2Lo + kB2W + sslot * 256);
   };
   // operand read offsets: hi / lo chunks 2kg + t of row lr (slot_key8), W2 chunk kg of row lr (bg_key4)
   const int rh0 = lr * 128 + (((2 * kg) ^ slot_key8(lr)) * 16);
@@ -1175,10 +1209,9 @@ __device__ __forceinline__ void gemm2_big_unit(const Problem& pb, const Plan& pl
   v4f pp[NT][4];
   auto stage = [&](int j, auto first_c) {
     constexpr bool kFirst = decltype(first_c)::value;
-    // one stage in flight past the current one: kOps operations per wavefront
+    // one stage in flight past the current one: stage j + 1's DMAs (an odd stage's when j is even)
     static_assert(kB2Stages == 3, "wait count");
-    if constexpr (kOps == 5) MOEFP8_WAIT_VMCNT(5);
-    else MOEFP8_WAIT_VMCNT(7);
+    wait_vmcnt_2to7(kFirst ? n_odd : n_even);
     barrier_lds();
     const uint8_t* st = ring + (j % kB2Stages) * kB2Stage;
     v8h b16[4][2];
