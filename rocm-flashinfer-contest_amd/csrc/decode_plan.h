@@ -44,14 +44,21 @@ struct DecodePlanScratch {
 // count for both GEMMs at T = 1 and 4 (one and two local pairs: GEMM1 S = 8 / 4, GEMM2 S = 4 / 2;
 // per call 29.6 -> 29.2 and 37.3 -> 36.5 us against S <= 4 everywhere; S <= 8 everywhere had cost
 // 34.3 / 44.4 against 31.6 / 38.9, up to 20 splits 35.4 / 41.4).
+// `s_floor`: the fewest splits whose K ranges fit the staged path's LDS rows (kPreMaxKB /
+// kPre2MaxKB K-blocks), kept even where one resident round would hold fewer units: GEMM1 at
+// T = 64 (19 m-tiles, S = 1 by the round) with S = 2 runs its m-tiles of <= 4 rows on the staged
+// path, 187.8 -> 183.9 us per call (GEMM2 with S = 2 there: +15 us, so its floor stays 1).
 constexpr int kDecMaxSplit = 4;
 constexpr int kDecFewSplit = 8;
-__device__ __forceinline__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap, int budget) {
+constexpr int kPreMaxKB = 28;    // K-blocks a GEMM1 unit can stage (staged path)
+constexpr int kPre2MaxKB = 16;   // the same for GEMM2
+__device__ __forceinline__ int pick_split(int n_mt, int ncb, int kb, int slots, int P, int rows_cap, int budget,
+                                          int s_floor) {
   const int s_min = (kb + kWave - 1) / kWave;
   const int per = n_mt * ncb;   // units per split
   int S = min(kb, kDecMaxSplit);
   if (per > 0 && 2 * per <= budget) S = min(kb, min(kDecFewSplit, budget / per));
-  else if (per > 0) S = min(S, slots / per);
+  else if (per > 0) S = min(S, max(s_floor, slots / per));
   if (P > 0) S = min(S, rows_cap / P);
   return max(S, s_min);
 }
@@ -129,8 +136,9 @@ __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, Dec
     if (lane == 0) {
       L.P = carry_p;
       L.n_mt = carry_mt;
-      L.S1 = pick_split(carry_mt, a.sp.ncb1, a.sp.kb1, a.sp.slots1, carry_p, a.sp.rows_cap1, a.sp.budget);
-      L.S2 = pick_split(carry_mt, a.sp.ncb2, a.sp.kb2, a.sp.slots2, carry_p, a.sp.rows_cap2, a.sp.budget);
+      L.S1 = pick_split(carry_mt, a.sp.ncb1, a.sp.kb1, a.sp.slots1, carry_p, a.sp.rows_cap1, a.sp.budget,
+                        (a.sp.kb1 + kPreMaxKB - 1) / kPreMaxKB);
+      L.S2 = pick_split(carry_mt, a.sp.ncb2, a.sp.kb2, a.sp.slots2, carry_p, a.sp.rows_cap2, a.sp.budget, 1);
       if (global) {
         a.expert_offsets[E] = carry_p;
         a.mtile_offsets[E] = carry_mt;

@@ -84,7 +84,6 @@ struct alignas(16) G1Stage {
 // bytes per lane group, GEMM2: 64) fall on distinct 16-byte bank groups whether the LDS serves
 // 8, 16 or 32 lanes at a time.
 constexpr int kPreRows = 4;
-constexpr int kPreMaxKB = 28;
 constexpr int kPre1RowBytes = kPreMaxKB * kBlock + 80;
 struct alignas(16) G1Pre {
   uint8_t a[kPreRows * kPre1RowBytes];
@@ -92,7 +91,6 @@ struct alignas(16) G1Pre {
 };
 
 // GEMM2's staged rows: C's f16 hi term, <= kPre2MaxKB K-blocks of 128 columns per unit.
-constexpr int kPre2MaxKB = 16;
 constexpr int kPre2RowBytes = kPre2MaxKB * kBlock * 2 + 16;
 struct alignas(16) G2Pre {
   uint8_t a[kPreRows * kPre2RowBytes];
