@@ -40,11 +40,11 @@ constexpr int kDec2BlocksPerCU = 5;          // GEMM2 too (<= 96 VGPRs: its per-
 constexpr int kDecDepth = 3;                 // K-blocks in flight per wavefront (register ring)
 static_assert(64 * kDecBlockWaves == kPlanThreads, "the GEMM1 workgroups build the plan");
 
-// One 16-byte chunk of a weight line on the staged paths.  Each weight byte is read once per
-// call and each 128-byte line by one load instruction (8 lanes), so the load carries the
-// non-temporal hint (streamed through L2): 5% less time per call at 16 tokens, measured.  The
-// per-step paths keep ordinary loads: their MFMA-layout loads split a line over two
-// instructions, and the hint evicts it in between (16% more time at 64 tokens, measured).
+// One 16-byte chunk of a weight line.  Each weight byte is read once per call and each 128-byte
+// line by one load instruction (8 lanes), so the load carries the non-temporal hint (streamed
+// through L2): 5% less time per call at 16 tokens, measured.  On loads that split a line over two
+// instructions (the MFMA layout, 16 rows x 64 bytes) the hint evicts it in between (16% more time
+// at 64 tokens, measured), so every weight stream loads whole lines.
 __device__ __forceinline__ v4i load_w_line(const uint8_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
 }
@@ -313,12 +313,23 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
       const float* ssrc = pb.hscale + (size_t)kb0 * T + tok;
       // weight scale of K-block kb0 + l in lane l (n <= 64), read per step with readlane
       const float swv = swp[min(lane, n - 1)];
-      v8i B[kStepDepth];
+      // weights as whole lines with the non-temporal hint, transposed per wavefront through its LDS
+      // buffer tb as on the staged path (MFMA-layout loads instead: 184.8 against 173.9 us per call
+      // at T = 64, both GEMMs, measured).  Chunk c of row r sits at r * 128 + (c ^ slot_key8(r)) * 16,
+      // so row wr + 8's chunk is at (tw0o ^ 16) + 1024 and chunk 2kg + 1 of row lr at trxo ^ 16
+      // (slot_key8(r + 8) = slot_key8(r) ^ 1 for r < 8): two offsets kept instead of four
+      const int wr = lane >> 3, wc = lane & 7;
+      const uint8_t* wsrc = pb.w13 + ((size_t)e * I2 + cg * 16 + wr) * H + (size_t)kb0 * kBlock + wc * 16;
+      uint8_t* const tb = wtr[wave];
+      const int tw0o = wr * kBlock + (wc ^ slot_key8(wr)) * 16;
+      const int trxo = lr * kBlock + ((2 * kg) ^ slot_key8(lr)) * 16;
+      v4i B0[kStepDepth], B1[kStepDepth];
       v4i AR[kStepDepth];
       float SR[kStepDepth];
       auto load = [&](int d, int j) {
         const int jj = min(j, n - 1);
-        B[d] = load_v8i(bp + (size_t)jj * kBlock);
+        B0[d] = load_w_line(wsrc + (size_t)jj * kBlock);
+        B1[d] = load_w_line(wsrc + (size_t)jj * kBlock + (size_t)8 * H);
         AR[d] = *reinterpret_cast<const v4i*>(asrc + (size_t)jj * astep);
         SR[d] = ssrc[(size_t)jj * T];
       };
@@ -326,12 +337,20 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
         G1Stage& st = ring[j & 1];
         if (wave < 2) *reinterpret_cast<v4i*>(st.a + ar * kBlock + ((lane & 7) ^ slot_key8(ar)) * 16) = AR[d];
         if (wave == 0 && lane < 16) st.sa[lane] = SR[d];
+        // (formed per step: four live offsets spilled at the 96-VGPR budget)
+        int t0 = tw0o, t1 = trxo;
+        asm volatile("" : "+v"(t0), "+v"(t1));
+        *reinterpret_cast<v4i*>(tb + t0) = B0[d];
+        *reinterpret_cast<v4i*>(tb + ((t0 ^ 16) + 1024)) = B1[d];
         __syncthreads();
+        const v4i bx = *reinterpret_cast<const v4i*>(tb + t1);
+        const v4i by = *reinterpret_cast<const v4i*>(tb + (t1 ^ 16));
         const v4i x = *reinterpret_cast<const v4i*>(st.a + lr * kBlock + ((2 * kg) ^ slot_key8(lr)) * 16);
         const v4i y = *reinterpret_cast<const v4i*>(st.a + lr * kBlock + ((2 * kg + 1) ^ slot_key8(lr)) * 16);
         const float4 sa = *reinterpret_cast<const float4*>(st.sa + 4 * kg);
         const float sw = readlane_f32(swv, j);
-        const v4f p = mfma16x16x128(__builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7), B[d],
+        const v4f p = mfma16x16x128(__builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7),
+                                    __builtin_shufflevector(bx, by, 0, 1, 2, 3, 4, 5, 6, 7),
                                     v4f{0.f, 0.f, 0.f, 0.f});
         acc[0] += p[0] * (sa.x * sw);
         acc[1] += p[1] * (sa.y * sw);
@@ -606,12 +625,23 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       const _Float16* asrc = ch.hi + (size_t)(row0 + (ar < M ? ar : 0)) * I + (size_t)kb0 * kBlock + (lane & 15) * 8;
       const float* ssrc = ch.scale + (size_t)prow * KB + kb0;
       const float swv = swp[min(lane, n - 1)];
-      v8i B[kStepDepth2];
+      // weights as whole lines with the non-temporal hint, transposed per wavefront through its LDS
+      // buffer tb as on the staged path (MFMA-layout loads instead: 184.8 against 173.9 us per call
+      // at T = 64, both GEMMs, measured).  Chunk c of row r sits at r * 128 + (c ^ slot_key8(r)) * 16,
+      // so row wr + 8's chunk is at (tw0o ^ 16) + 1024 and chunk 2kg + 1 of row lr at trxo ^ 16
+      // (slot_key8(r + 8) = slot_key8(r) ^ 1 for r < 8): two offsets kept instead of four
+      const int wr = lane >> 3, wc = lane & 7;
+      const uint8_t* wsrc = pb.w2 + ((size_t)e * H + cg * 16 + wr) * I + (size_t)kb0 * kBlock + wc * 16;
+      uint8_t* const tb = wtr[wave];
+      const int tw0o = wr * kBlock + (wc ^ slot_key8(wr)) * 16;
+      const int trxo = lr * kBlock + ((2 * kg) ^ slot_key8(lr)) * 16;
+      v4i B0[kStepDepth2], B1[kStepDepth2];
       v4i AR[kStepDepth2];
       float SR[kStepDepth2];
       auto load = [&](int d, int j) {
         const int jj = min(j, n - 1);
-        B[d] = load_v8i(bp + (size_t)jj * kBlock);
+        B0[d] = load_w_line(wsrc + (size_t)jj * kBlock);
+        B1[d] = load_w_line(wsrc + (size_t)jj * kBlock + (size_t)8 * I);
         AR[d] = *reinterpret_cast<const v4i*>(asrc + (size_t)jj * kBlock);
         SR[d] = ssrc[jj];
       };
@@ -619,19 +649,36 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
         G2Stage& st = ring[j & 1];
         *reinterpret_cast<v4i*>(st.a + ar * (2 * kBlock) + ((lane & 15) ^ slot_key16(ar)) * 16) = AR[d];
         if (wave == 0 && lane < 16) st.sa[lane] = SR[d];
+        // (formed per step: four live offsets spilled at the 96-VGPR budget)
+        int t0 = tw0o, t1 = trxo;
+        asm volatile("" : "+v"(t0), "+v"(t1));
+        *reinterpret_cast<v4i*>(tb + t0) = B0[d];
+        *reinterpret_cast<v4i*>(tb + ((t0 ^ 16) + 1024)) = B1[d];
         __syncthreads();
+        const v4i bx = *reinterpret_cast<const v4i*>(tb + t1);
+        const v4i by = *reinterpret_cast<const v4i*>(tb + (t1 ^ 16));
         // chunk 4 kg + t sits at byte (4 kg ^ key) * 16 ^ 16 t of the row: one base register,
         // formed here (hoisted, the four addresses stay live across the loop and spill)
         int rb = lr * (2 * kBlock) + ((4 * kg) ^ slot_key16(lr)) * 16;
         asm volatile("" : "+v"(rb));
-        v8h ah[4];
-#pragma unroll
-        for (int t = 0; t < 4; t++) ah[t] = *reinterpret_cast<const v8h*>(st.a + (rb ^ (16 * t)));
         const float4 sa = *reinterpret_cast<const float4*>(st.sa + 4 * kg);
         const float sw = readlane_f32(swv, j);
-        v8h b16[4];
-        widen_fp8_operand(B[d], b16);
-        const v4f p = mfma_f16_block(ah, b16, v4f{0.f, 0.f, 0.f, 0.f});
+        // one 32-K piece at a time (C's hi chunk, the W2 chunk widened exactly, their MFMA), in
+        // the order of widen_fp8_operand + mfma_f16_block: all four pieces widened at once
+        // spilled 4 VGPRs
+        v4f p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const v8h ah = *reinterpret_cast<const v8h*>(st.a + (rb ^ (16 * t)));
+          const uint32_t w0 = (uint32_t)(t < 2 ? bx[2 * t] : by[2 * t - 4]);
+          const uint32_t w1 = (uint32_t)(t < 2 ? bx[2 * t + 1] : by[2 * t - 3]);
+          const v2h l0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false);
+          const v2h h0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true);
+          const v2h l1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false);
+          const v2h h1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true);
+          const v8h b = {l0[0], l0[1], h0[0], h0[1], l1[0], l1[1], h1[0], h1[1]};
+          p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, p, 0, 0, 0);
+        }
         acc[0] += p[0] * (sa.x * sw);
         acc[1] += p[1] * (sa.y * sw);
         acc[2] += p[2] * (sa.z * sw);
