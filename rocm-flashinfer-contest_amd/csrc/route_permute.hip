@@ -243,7 +243,8 @@ __device__ void route_token(const float (&x)[4], const float (&b)[4], float rsf,
 
 // Blocks in order: one per local expert for the weight-scale estimates, then, with the magnitude
 // inputs, the hidden-row norm blocks, then the routing blocks (the two leading kinds first, so
-// that they run beside the routing blocks instead of after them).  Norm and routing blocks take
+// that they run beside the routing blocks instead of after them; at T <= 64 the dispatch order is
+// rotated to put the routing blocks first).  Norm and routing blocks take
 // one token per wavefront (kSigmaThreads / 64 tokens per block): the norm streams the hidden
 // rows while the routing arithmetic runs on other wavefronts.
 __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __restrict__ logits, int logits_dt,
@@ -256,19 +257,23 @@ __global__ __launch_bounds__(kSigmaThreads) void route_kernel(const void* __rest
   const int lane = lane_id();
   const int wave = threadIdx.x >> 6;
   constexpr int kWavesPerBlock = kSigmaThreads / kWave;
-  if ((int)blockIdx.x < sigma_blocks) {
-    expert_sigma_block(mg, blockIdx.x);
+  // At T <= 64 every block is resident at once and the few routing blocks are the launch's
+  // critical path, so they are dispatched first (route stage -0.2-0.3 us, measured); at large T
+  // the leading sigma and norm blocks must not wait behind thousands of routing blocks.
+  const int bid = T <= 64 ? ((int)blockIdx.x + sigma_blocks + norm_blocks) % (int)gridDim.x : (int)blockIdx.x;
+  if (bid < sigma_blocks) {
+    expert_sigma_block(mg, bid);
     return;
   }
-  if ((int)blockIdx.x < sigma_blocks + norm_blocks) {
-    const int nb = (int)blockIdx.x - sigma_blocks;
+  if (bid < sigma_blocks + norm_blocks) {
+    const int nb = bid - sigma_blocks;
     for (int64_t t = (int64_t)nb * kWavesPerBlock + wave; t < T; t += (int64_t)norm_blocks * kWavesPerBlock) {
       const float a2 = token_sq_norm(mg.hidden, mg.hscale, mg.H, T, t);
       if (lane == 0) mg.tok_a2[t] = a2;
     }
     return;
   }
-  const int tb = (int)blockIdx.x - sigma_blocks - norm_blocks;   // routing block
+  const int tb = bid - sigma_blocks - norm_blocks;   // routing block
   for (int i = tb * kSigmaThreads + threadIdx.x; i < n_zero; i += token_blocks * kSigmaThreads)
     zero[(size_t)i * kCounterStride] = 0;
   // the first token's logits (a clamped row: no branch) leave with the bias, one round trip
