@@ -16,7 +16,8 @@ extra event packets sit between the kernels.  A third pass times the drop-in
 ``moe_fp8.run(...)`` itself (argument checks, output and workspace allocation,
 ctypes) the way the reference's harness times a solution (flush, event, call,
 event, back to back): ``run_us_per_call``; ``run_host_us_per_call`` is the host
-time of one call.
+time of one call.  A fourth pass replays the call captured in a HIP graph, cold like the
+others (``graph_us_per_call``), as a serving loop that captures its decode step runs it.
 
 Prints ONE JSON line.  Headline: T=16 decode (H=7168, I=2048, 32 local experts),
 in us/call; the T=8192 large-prefill line and the other synthetic workloads
@@ -145,6 +146,23 @@ def measure(wl, weights, steps, warmup, flush):
     e_b.record()
     torch.cuda.synchronize()
     warm_us = e_a.elapsed_time(e_b) * 1e3 / steps
+    # the same call captured once in a HIP graph and replayed cold (flush, event, replay, event),
+    # as a serving loop runs its decode step: the launches leave as one graph instead of one
+    # stream packet each.  Reported beside the eager figure, which stays the per-call time.
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        runner()
+    torch.cuda.synchronize()
+    gs = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ge = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for i in range(steps):
+        evict()
+        gs[i].record()
+        graph.replay()
+        ge[i].record()
+    torch.cuda.synchronize()
+    graph_us = statistics.median(gs[i].elapsed_time(ge[i]) * 1e3 for i in range(steps))
+    del graph
     # the drop-in entry point itself, as the reference's harness times a solution's run()
     # (flush, event, run(...), event, back to back without host synchronisation; its argument
     # checks, output allocation and ctypes call overlap the flush still running on the device),
@@ -173,7 +191,7 @@ def measure(wl, weights, steps, warmup, flush):
     st = {s: statistics.median(v) for s, v in stages.items()}
     res = dict(workload=wl.name, T=T, us_per_call=us, us_min=min(per_step), us_max=max(per_step),
                us_mean=statistics.fmean(per_step), warm_us_per_call=warm_us, host_wall_s=wall,
-               run_us_per_call=run_us, run_host_us_per_call=run_host_us,
+               run_us_per_call=run_us, run_host_us_per_call=run_host_us, graph_us_per_call=graph_us,
                stages_us=st, **wk)
     res["tflops"] = wk["flops"] / (us * 1e-6) / 1e12
     res["gbps"] = wk["bytes"] / (us * 1e-6) / 1e9
@@ -388,6 +406,7 @@ def main():
         "warm_us_per_call": round(head["warm_us_per_call"], 2),
         "run_us_per_call": round(head["run_us_per_call"], 2),
         "run_host_us_per_call": round(head["run_host_us_per_call"], 2),
+        "graph_us_per_call": round(head["graph_us_per_call"], 2),
         "gemm_fracs": head["gemm_fracs"],
         "roofline": head["roofline"],
         "cpu_baseline": cpu,
@@ -395,7 +414,7 @@ def main():
     if sec is not None:
         line["t8192"] = {k: sec[k] for k in ("us_per_call", "tflops", "gbps", "hbm_frac", "mfma_frac", "roofline_frac",
                                            "active_experts", "pairs", "stages_us", "gemm_fracs", "roofline",
-                                           "run_us_per_call", "run_host_us_per_call")}
+                                           "run_us_per_call", "run_host_us_per_call", "graph_us_per_call")}
     if quant is not None:
         line["quantize_hidden"] = quant
     if sweep:
@@ -404,6 +423,7 @@ def main():
                              "hbm_frac": round(v["hbm_frac"], 4), "mfma_frac": round(v["mfma_frac"], 4),
                              "run_us_per_call": round(v["run_us_per_call"], 2),
                              "run_host_us_per_call": round(v["run_host_us_per_call"], 2),
+                             "graph_us_per_call": round(v["graph_us_per_call"], 2),
                              "P": v["pairs"], "A": v["active_experts"],
                              "stages_us": {s: round(x, 1) for s, x in v["stages_us"].items()}}
                          for k, v in sweep.items()}
