@@ -13,6 +13,7 @@
 namespace moefp8 {
 
 constexpr int kSmallT = 64;
+static_assert(kSmallT <= 256, "pair tokens are stored as bytes");
 constexpr int kSmallTile = 16;
 constexpr int kSmallPairs = kSmallT * kTopK;
 constexpr int kSmallMaxMtiles = kSmallPairs / kSmallTile + kEGlobal;
@@ -21,7 +22,10 @@ constexpr int kPlanThreads = 256;   // threads of a workgroup that builds the pl
 // What the GEMM reads while it runs ...
 struct DecodePlanLds {
   int4 mt[kSmallMaxMtiles];             // {expert, first pair row, rows, OR of pair flags}
-  int tok[kSmallPairs];                 // token of each pair row
+  // token of each pair row (T <= 64), as bytes: with ints the workgroup's LDS (32,024 B) no
+  // longer let five workgroups share a CU (an empty GEMM1 launch 1 us slower, measured)
+  uint8_t tok[kSmallPairs];
+  float w[kSmallPairs];                 // routing weight of each pair row
   int n_mt, P, S1, S2;
 };
 // ... and what only the build uses (free for other use once it returns).
@@ -171,6 +175,7 @@ __device__ void build_decode_plan(const DecodePlanArgs& a, DecodePlanLds& L, Dec
       const int pos = X.base[le] + (int)__popcll(X.tmask[le] & ((1ull << t) - 1ull));
       L.tok[pos] = t;
       const float w = X.w[i];
+      L.w[pos] = w;
       const float pred = predicted_output_rms(X.a2[t], w, X.esig[2 * le], X.esig[2 * le + 1], a.sqrt_i);
       const int flags = (pred > kPreciseRms ? kFlagExactProducts : 0) | (pred > kOneTermRms ? kFlagTwoTermC : 0);
       if (flags) atomicOr(&L.mt[X.mtb[le] + (pos - X.base[le]) / kSmallTile].w, flags);

@@ -406,20 +406,16 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
     }
     // C columns [128 j, 128 j + 128) of the m-tile need the partials of 4 S units: column
     // blocks 2j, 2j + 1 ("up") and NCB/2 + 2j, NCB/2 + 2j + 1 ("gate"), S K-splits each.
-    // Every unit publishes its partials and counts itself in; the last one forms C.
+    // Every unit publishes its partials and counts itself in; the last one forms C.  The pairs'
+    // routing weights come from the plan in LDS, so after the arrival the last unit's one round
+    // trip to memory is the partials (with the expert's W2 estimate, needed only at the end):
+    // -0.6 / -1.0 / -0.35 / -1.5 us per call at T = 1 / 4 / 16 / 64 against reading them from
+    // the routing outputs (measured).
     const int j = (du.cb % (NCB / 2)) / 2;
     if (arrive_last(pl.counters + (du.g * (I / kBlock) + j) * kCounterStride, 4 * S, &last_s)) {
       const float sigma2 = da.esig[2 * e + 1];
-      for (int r = wave; r < M; r += kDecBlockWaves) {
-        // the pair's routing weight: its token's slot holding this expert (the routing outputs
-        // are complete before this launch)
-        const int t = plan.tok[row0 + r];
-        float w = 0.f;
-#pragma unroll
-        for (int k = 0; k < kTopK; k++)
-          if (da.topk_ids[t * kTopK + k] - da.offset == e) w = da.topk_w[t * kTopK + k];
-        swiglu_block(I, S, row0 + r, j, gbuf, ch, w, sigma2, pl.two_term + du.g * kCounterStride);
-      }
+      for (int r = wave; r < M; r += kDecBlockWaves)
+        swiglu_block(I, S, row0 + r, j, gbuf, ch, plan.w[row0 + r], sigma2, pl.two_term + du.g * kCounterStride);
     }
   }
 }
@@ -734,7 +730,9 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       }
     }
     // output columns [64 cb, 64 cb + 64) are complete once all n_mt * S units of the column
-    // block stored their rows
+    // block stored their rows.  (Every unit loading its first combine pass's token slots before
+    // the arrival, so the last one skips that round trip: +0.3 us at T = 16, +1.4 at 64, measured;
+    // all units of the launch then read the same few lines.)
     if (arrive_last(pl.counters2 + du.cb * kCounterStride, n_mt * S, &last_s))
       combine_columns(pl.tok_slot, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves, pl.shared, pl.shared_dt,
                       pl.out_f32, pl.info[0]);
