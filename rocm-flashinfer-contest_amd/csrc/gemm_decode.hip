@@ -421,11 +421,12 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec1BlocksPerCU) void gemm1_d
 }
 
 // Combine of output columns [c0, c0 + 64) for every token by one workgroup (main.py:241-243):
-// each token's pair rows in ascending local-expert order (tok_slot), the K-split partials of
-// a row first, summed from zero in fp32 and rounded once to bf16; tokens without a local
-// expert get zeros.  Thread = (token, 4 columns).  Pair indices read from tok_slot are clamped below
-// pair_rows (the call's pair count: rows pair_rows * S of the partials are written).
-__device__ void combine_columns(const int* __restrict__ tok_slot, const float* __restrict__ obuf,
+// each token's pair rows in ascending local-expert order (tok_slot, here its copy in LDS), the
+// K-split partials of a row first, summed from zero in fp32 and rounded once to bf16; tokens
+// without a local expert get zeros.  Thread = (token, 4 columns).  Pair indices read from
+// tok_slot are clamped below pair_rows (the call's pair count: rows pair_rows * S of the partials
+// are written).
+__device__ void combine_columns(const int* tok_slot_lds, const float* __restrict__ obuf,
                                 void* __restrict__ out, int T, int H, int S, int c0, const void* shared,
                                 int shared_dt, int out_f32, int pair_rows) {
   constexpr int kQuads = 16;                            // 4-column groups of the 64 columns
@@ -433,7 +434,7 @@ __device__ void combine_columns(const int* __restrict__ tok_slot, const float* _
   for (int t = threadIdx.x / kQuads; t < T; t += blockDim.x / kQuads) {
     int slots[kTopK];
 #pragma unroll
-    for (int k = 0; k < kTopK; k++) slots[k] = tok_slot[(size_t)t * kTopK + k];
+    for (int k = 0; k < kTopK; k++) slots[k] = tok_slot_lds[t * kTopK + k];
     float4 acc = {0.f, 0.f, 0.f, 0.f};
     if (S == 1) {
       // the token's (at most 8) rows loaded together; a token's unused slots are -1 and last
@@ -499,6 +500,8 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
   __shared__ int last_s;
   // per-wavefront weight transpose buffers of the staged path (16 rows x 128 bytes)
   __shared__ __attribute__((aligned(16))) uint8_t wtr[kDecBlockWaves][16 * kBlock];
+  // every token's pair rows (tok_slot) for the combine
+  __shared__ __attribute__((aligned(16))) int slot_s[kSmallT * kTopK];
   G2Stage* ring = sh.ring;
   const int n_mt = pl.info[2], S = pl.info[4];
   const int H = pb.H, I = pb.I, T = pb.T;
@@ -514,6 +517,18 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
       store_out4(out, 4 * i, acc, pl.out_f32);
     }
     return;
+  }
+
+  // tok_slot (T x 8 ints, <= 2 KB) copied into LDS by DMA (waves 0 and 1, 1 KB each), issued
+  // before the first unit: nothing waits for it until a combine, which follows the arrival's wait
+  // for all of the workgroup's memory operations and a barrier, so the last unit of a column
+  // block goes straight to the pair rows (one round trip less per combine pass).  The oldest
+  // operation in flight, it only makes the waits of the compiler's own loads more conservative
+  // until it lands.
+  if ((int)blockIdx.x < n_units && wave * kWave * 4 < T * kTopK) {
+    const uint32_t bytes = (uint32_t)(T * kTopK * 4);
+    const uint32_t off = min((uint32_t)(wave * kWave + lane_id()) * 16u, bytes - 16u);
+    dma_lds16_s(off, pl.tok_slot, uniform((int)lds_addr(slot_s)) + (uint32_t)(wave * kWave * 16));
   }
 
   for (int u = blockIdx.x; u < n_units; u += gridDim.x) {
@@ -734,7 +749,7 @@ __global__ __launch_bounds__(64 * kDecBlockWaves, kDec2BlocksPerCU) void gemm2_d
     // the arrival, so the last one skips that round trip: +0.3 us at T = 16, +1.4 at 64, measured;
     // all units of the launch then read the same few lines.)
     if (arrive_last(pl.counters2 + du.cb * kCounterStride, n_mt * S, &last_s))
-      combine_columns(pl.tok_slot, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves, pl.shared, pl.shared_dt,
+      combine_columns(slot_s, obuf, out, T, H, S, du.cb * 16 * kDecBlockWaves, pl.shared, pl.shared_dt,
                       pl.out_f32, pl.info[0]);
   }
 }

@@ -92,34 +92,6 @@ __device__ __forceinline__ void lds_read5(uint32_t a0, uint32_t a1, uint32_t a2,
       : "memory");
 }
 
-__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
-
-// DMA and its completion wait as inline asm, for kernels whose LDS operand reads are ordinary
-// loads: the compiler then neither knows of the DMAs nor drains them before every LDS read, and
-// schedules the reads with exact lgkmcnt waits.  The writer of M0 must precede the DMA by one
-// wait state.
-__device__ __forceinline__ void dma_lds16(const void* g, uint32_t lds_uniform) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(lds_uniform)
-               : "memory", "m0");
-}
-__device__ __forceinline__ void dma_lds4(const void* g, uint32_t lds_uniform) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(lds_uniform)
-               : "memory", "m0");
-}
-// The same with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane byte offset.
-__device__ __forceinline__ void dma_lds16_s(uint32_t voff, const void* sbase, uint32_t lds_uniform) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(sbase),
-               "s"(lds_uniform) : "memory", "m0");
-}
-// The same with the non-temporal hint (streamed through L2), for lines read once per call.
-__device__ __forceinline__ void dma_lds16_s_nt(uint32_t voff, const void* sbase, uint32_t lds_uniform) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" : : "v"(voff), "s"(sbase),
-               "s"(lds_uniform) : "memory", "m0");
-}
-__device__ __forceinline__ void dma_lds4_s(uint32_t voff, const void* sbase, uint32_t lds_uniform) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(voff), "s"(sbase),
-               "s"(lds_uniform) : "memory", "m0");
-}
 // s_barrier, then no memory access may move above it
 __device__ __forceinline__ void barrier_lds() {
   __builtin_amdgcn_s_barrier();
